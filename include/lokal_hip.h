@@ -1,0 +1,230 @@
+/*
+ * lokal_hip.h -- C ABI of the MI355X (gfx950) decode backend for lokal.
+ *
+ * The boundary is lokal's backend seam, src/engine.rs:13-71 (Engine, Session,
+ * Batcher, BatchRow) plus the quantized-GGUF constructor create_metal_quant
+ * (src/engine.rs:150-162).  Every function returns 0 on success or a negative
+ * LKHIP_E* code; lkhip_last_error() then holds a one-line, thread-local reason
+ * in the reference's refusal style (src/engine.rs:105-109, src/main.rs:326-355).
+ *
+ * Ownership: the caller owns every host buffer passed in or out.  Sessions and
+ * batches borrow their engine (Session<'_> in src/engine.rs:18) and must be
+ * destroyed before it.  An engine is safe to share across threads for session
+ * creation; a session or batch is single-threaded and owns its HIP stream.
+ *
+ * Pointer kinds: functions under "engine / session / batch" take HOST pointers.
+ * The kernel-level functions under "kernels" take DEVICE pointers (from
+ * lkhip_malloc) and a stream (NULL = the null stream) and do not synchronise.
+ */
+#ifndef LOKAL_HIP_H
+#define LOKAL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LKHIP_OK = 0,
+    LKHIP_E_INVALID = -1,     /* bad argument / shape */
+    LKHIP_E_UNSUPPORTED = -2, /* refused: type or shape this backend does not run */
+    LKHIP_E_HIP = -3,         /* HIP runtime error */
+    LKHIP_E_NOMEM = -4,       /* allocation failed */
+    LKHIP_E_IO = -5           /* file could not be read / parsed */
+};
+
+/* GGUF tensor type ids (enum ggml_type), src/gguf/dequant.rs:21-40. */
+enum {
+    LKHIP_F32 = 0,
+    LKHIP_F16 = 1,
+    LKHIP_Q8_0 = 8,
+    LKHIP_Q4_K = 12
+};
+
+/* ModelConfig, src/config.rs:10-30 (the fields the decode step reads).
+ * head_dim 0 means hidden_size / num_attention_heads (config.rs:92-95). */
+typedef struct lkhip_config {
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t num_hidden_layers;
+    uint32_t num_attention_heads;
+    uint32_t num_key_value_heads;
+    uint32_t vocab_size;
+    uint32_t head_dim;
+    uint32_t max_position_embeddings;
+    float rms_norm_eps;
+    float rope_theta;
+} lkhip_config;
+
+/* One named tensor as a TensorStore / GGUF tensor hands it over
+ * (src/weights.rs:77-97, src/gguf/dequant.rs:129-133): HF name, GGUF type id,
+ * row-major dims [rows, cols] (n_dims 1 => [cols]), raw little-endian bytes. */
+typedef struct lkhip_tensor {
+    const char* name;
+    uint32_t ggml_type;
+    uint32_t n_dims;
+    uint64_t dims[2];
+    const void* data;
+    uint64_t nbytes;
+} lkhip_tensor;
+
+/* BatchRow, src/engine.rs:30-34. */
+typedef struct lkhip_row {
+    uint32_t token;
+    uint32_t slot;
+    uint64_t pos;
+} lkhip_row;
+
+/* Per-session kernel timing, summed over every forward since the last reset
+ * (the HIP counterpart of LOKAL_GPU_TIMING's phase table, src/gpu/metal.rs:3856-3952). */
+typedef struct lkhip_profile {
+    uint64_t tokens;           /* forwards timed */
+    uint64_t matvec_launches;  /* dequant-matvec kernel launches */
+    double matvec_ms;          /* summed hipEvent time of those launches */
+    double matvec_bytes;       /* algorithmic weight bytes they read */
+    uint64_t lm_head_launches;
+    double lm_head_ms;         /* the single largest matvec, lm_head */
+    double lm_head_bytes;
+    double attn_ms;            /* flash-decoding partial + merge */
+    double other_ms;           /* norms, rope, gather, argmax */
+} lkhip_profile;
+
+typedef struct lkhip_engine lkhip_engine;
+typedef struct lkhip_session lkhip_session;
+typedef struct lkhip_batch lkhip_batch;
+typedef struct lkhip_weight lkhip_weight;
+
+/* ------------------------------------------------------------- general */
+
+/* Thread-local reason for the last failure on this thread ("" if none). */
+const char* lkhip_last_error(void);
+/* Number of visible HIP devices (0 with no GPU; never fails). */
+int lkhip_device_count(void);
+/* Library version string. */
+const char* lkhip_version(void);
+
+/* ------------------------------------------------- engine / session */
+
+/* Engine from named tensors (HF names as src/model.rs:160-186 reads them):
+ * weights upload once and stay resident (src/gpu/mod.rs:9-10).  Linear
+ * weights may be F16, Q8_0 or Q4_K; norms and biases F32 (or F16).  A missing
+ * lm_head.weight ties it to model.embed_tokens.weight (src/model.rs:181-186).
+ * llama_permuted != 0 undoes llama.cpp's q/k row permute at upload
+ * (src/gguf/arch.rs:274-286, applied as in src/gguf/dequant.rs:548-553).
+ * Replaces engine::create (src/engine.rs:76-111) for the "hip" backend. */
+int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_tensor* tensors, size_t n_tensors,
+                                int llama_permuted, lkhip_engine** out);
+/* Engine straight from a GGUF v2/v3 file; weights stay quantized on device.
+ * Replaces create_metal_quant (src/engine.rs:150-162) / MetalEngine::new_gguf_quant
+ * (src/gpu/metal.rs:1667); config from GGUF metadata as gguf::model_config does
+ * (src/gguf/arch.rs:164-223). */
+int lkhip_engine_create_gguf(const char* path, lkhip_engine** out);
+void lkhip_engine_destroy(lkhip_engine* e);
+/* Engine::config (src/engine.rs:15). */
+int lkhip_engine_config(const lkhip_engine* e, lkhip_config* out);
+/* Algorithmic bytes of every weight one decode token reads (matvecs only). */
+double lkhip_engine_matvec_bytes(const lkhip_engine* e);
+
+/* Engine::session (src/engine.rs:17): KV cache (f16, on device) for max_seq positions. */
+int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_session** out);
+void lkhip_session_destroy(lkhip_session* s);
+/* Session::forward (src/engine.rs:51): one token at pos -> vocab logits (host). */
+int lkhip_session_forward(lkhip_session* s, uint32_t token, size_t pos, float* logits_out);
+/* Session::prefill (src/engine.rs:56-62): the token loop; logits of the last
+ * position into logits_out (may be NULL). */
+int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size_t n, float* logits_out);
+/* Session::forward_batch (src/engine.rs:67-70): logits for every position,
+ * n * vocab floats. */
+int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n, size_t pos0, float* logits_out);
+/* The greedy decode loop of generate.rs:101-118 at -t 0 (argmax, first max
+ * wins, src/sampler.rs:67-75), run on the device: feeds `token` at `pos`, then
+ * feeds each argmax back, n_steps times; writes the n_steps argmax ids.  No
+ * host round trip per token.  logits_last (may be NULL) gets the final logits. */
+int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, size_t pos, size_t n_steps, uint32_t* ids_out,
+                                float* logits_last);
+/* Read back the f16 KV cache row of one layer at pos as f32 (kv_dim values). */
+int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int which_v, float* out);
+/* Kernel timing: on != 0 brackets every launch with hipEvents (eager launches,
+ * no graph) until switched off; profile_get sums since the last reset. */
+int lkhip_session_set_profiling(lkhip_session* s, int on);
+int lkhip_session_profile(lkhip_session* s, lkhip_profile* out, int reset);
+
+/* Engine::batcher (src/engine.rs:23-26): n_slots KV slots of max_seq positions,
+ * pool laid out per layer as [slot][kv_head][max_seq][head_dim] f16. */
+int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_seq, lkhip_batch** out);
+void lkhip_batch_destroy(lkhip_batch* b);
+/* Batcher::prefill (src/engine.rs:44): fill one slot with a prompt. */
+int lkhip_batch_prefill(lkhip_batch* b, uint32_t slot, const uint32_t* ids, size_t n, float* logits_out);
+/* Batcher::decode_step (src/engine.rs:46): one token per row; one weight read
+ * serves every row.  logits_out holds n_rows * vocab floats, in row order. */
+int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, float* logits_out);
+
+/* ------------------------------------------------------------ memory */
+
+int lkhip_malloc(void** dptr, size_t bytes);
+int lkhip_free(void* dptr);
+int lkhip_memcpy_htod(void* dst, const void* src, size_t bytes);
+int lkhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int lkhip_memset(void* dptr, int value, size_t bytes);
+int lkhip_synchronize(void);
+/* Streams at default priority and events for timing kernel-level calls. */
+int lkhip_stream_create(void** stream);
+int lkhip_stream_destroy(void* stream);
+int lkhip_stream_synchronize(void* stream);
+int lkhip_event_create(void** ev);
+int lkhip_event_destroy(void* ev);
+int lkhip_event_record(void* ev, void* stream);
+int lkhip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ----------------------------------------------------------- kernels */
+
+/* A weight matrix uploaded once in its GGUF type and repacked for the device
+ * (values unchanged).  type F16, Q8_0 or Q4_K; host bytes are GGUF rows. */
+int lkhip_weight_create(uint32_t ggml_type, size_t rows, size_t cols, const void* host_bytes, size_t nbytes,
+                        lkhip_weight** out);
+void lkhip_weight_destroy(lkhip_weight* w);
+/* Algorithmic bytes of the weight in its GGUF type. */
+double lkhip_weight_bytes(const lkhip_weight* w);
+
+/* dequant_row_ref (src/gguf/dequant.rs:191-535) for rows [row0, row0+n_rows):
+ * out is n_rows * cols f32, bit-exact with the CPU dequant. */
+int lkhip_dequant_rows(const lkhip_weight* w, size_t row0, size_t n_rows, float* out, void* stream);
+/* Linear::forward (src/model.rs:27-35) with the weight dequantized in the load:
+ * y[o] = dot(W[o,:], x) (+ bias[o]); accumulate != 0 adds into y instead
+ * (the residual add of src/model.rs:235-237, :253-255).  fp32 accumulation. */
+int lkhip_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate, void* stream);
+/* Typed forms of lkhip_matvec that refuse any other weight type. */
+int lkhip_q8_0_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
+                      void* stream);
+int lkhip_q4_k_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
+                      void* stream);
+/* math::rmsnorm (src/math.rs:45-49) over n_rows rows of n: y = x*s*w. */
+int lkhip_rmsnorm(const float* x, const float* w, size_t n_rows, size_t n, float eps, float* y, void* stream);
+/* model::rope (src/model.rs:268-279) in place on n_rows rows of n floats
+ * (n a multiple of head_dim); row r rotates at position pos[r] (device u32). */
+int lkhip_rope_pairs(float* x, size_t n_rows, size_t n, size_t head_dim, const uint32_t* pos, float theta,
+                     void* stream);
+/* SwiGLU of src/model.rs:247-249 with math::silu (src/math.rs:68-70):
+ * out[i] = silu(g[i]) * u[i], n elements. */
+int lkhip_swiglu(const float* g, const float* u, size_t n, float* out, void* stream);
+/* Embedding lookup, src/model.rs:200-202: out[r,:] = f32(table[ids[r],:]) for
+ * n_ids ids (device u32); the table is a weight of any supported type. */
+int lkhip_embed_gather(const lkhip_weight* table, const uint32_t* ids, size_t n_ids, float* out, void* stream);
+/* model::attention (src/model.rs:286-318) by flash-decoding for n_seq
+ * independent sequences, one query token each.  q: [n_seq][n_heads*head_dim]
+ * f32; k_cache/v_cache: f16 [n_seq][n_kv_heads][max_seq][head_dim]; ctx_len
+ * (device u32, n_seq) = positions 0..ctx_len-1 are live; out like q.
+ * head_dim must be 64; n_heads a multiple of n_kv_heads, group <= 8. */
+int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
+                      size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq, float* out,
+                      void* stream);
+/* Greedy argmax (src/sampler.rs:67-75, first max wins) of n_rows rows of n. */
+int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOKAL_HIP_H */

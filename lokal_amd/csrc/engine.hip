@@ -1,0 +1,967 @@
+// engine.hip -- host side of the HIP backend behind the C ABI of
+// include/lokal_hip.h: weight upload/repack, Engine / Session / Batcher
+// (src/engine.rs:13-71), the per-token launch sequence of Model::forward
+// (src/model.rs:196-262), HIP-graph replay, and the kernel-level entry points.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/lokal_hip.h"
+#include "lkhip_common.h"
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_OR_FAIL(expr)                                                                                  \
+    do {                                                                                                   \
+        hipError_t _e = (expr);                                                                            \
+        if (_e != hipSuccess) return fail(LKHIP_E_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));     \
+    } while (0)
+
+extern "C" const char* lkhip_last_error(void) { return g_err.c_str(); }
+extern "C" const char* lkhip_version(void) { return "lokal-hip 0.1 (gfx950)"; }
+extern "C" int lkhip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+// ------------------------------------------------------------------ weights
+
+struct lkhip_weight {
+    LkDevW dw{};
+    void* data = nullptr;
+    void* aux = nullptr;
+    double bytes = 0;  // algorithmic bytes in the GGUF type
+    ~lkhip_weight() {
+        if (data) (void)hipFree(data);
+        if (aux) (void)hipFree(aux);
+    }
+};
+
+static size_t blk_elems(uint32_t t) {
+    switch (t) {
+    case LKHIP_F32: case LKHIP_F16: return 1;
+    case LKHIP_Q8_0: return 32;
+    case LKHIP_Q4_K: return 256;
+    default: return 0;
+    }
+}
+static size_t blk_bytes(uint32_t t) {
+    switch (t) {
+    case LKHIP_F32: return 4;
+    case LKHIP_F16: return 2;
+    case LKHIP_Q8_0: return 34;
+    case LKHIP_Q4_K: return 144;
+    default: return 0;
+    }
+}
+static const char* type_name(uint32_t t) {
+    switch (t) {
+    case LKHIP_F32: return "F32";
+    case LKHIP_F16: return "F16";
+    case LKHIP_Q8_0: return "Q8_0";
+    case LKHIP_Q4_K: return "Q4_K";
+    case 2: return "Q4_0";
+    case 6: return "Q5_0";
+    case 13: return "Q5_K";
+    case 14: return "Q6_K";
+    default: return "unknown";
+    }
+}
+
+// Row order of a llama.cpp-permuted q/k weight: device row j of head h reads
+// source row h*hd + (j % (hd/2))*2 + j/(hd/2) (unpermute_llama_qk,
+// src/gguf/arch.rs:274-286).
+static size_t src_row(size_t r, size_t head_dim) {
+    if (!head_dim) return r;
+    const size_t h = r / head_dim, j = r % head_dim;
+    return h * head_dim + (j % (head_dim / 2)) * 2 + j / (head_dim / 2);
+}
+
+// Repack GGUF rows into the device layout (values unchanged) and upload.
+static int weight_create(uint32_t type, size_t rows, size_t cols, const void* host, size_t nbytes,
+                         size_t unpermute_hd, lkhip_weight** out) {
+    if (!host || !out || rows == 0 || cols == 0) return fail(LKHIP_E_INVALID, "weight: empty tensor or null pointer");
+    if (blk_elems(type) == 0)
+        return fail(LKHIP_E_UNSUPPORTED,
+                    "tensor type %s is not supported by the hip backend — re-quantize as Q8_0 or Q4_K (or F16)",
+                    type_name(type));
+    if (cols % blk_elems(type))
+        return fail(LKHIP_E_INVALID, "weight: %zu columns is not a whole number of %s blocks", cols, type_name(type));
+    if (type == LKHIP_F16 && cols % 8)
+        return fail(LKHIP_E_UNSUPPORTED, "F16 weight rows must hold a multiple of 8 values (got %zu)", cols);
+    const size_t row_bytes = cols / blk_elems(type) * blk_bytes(type);
+    if (nbytes != rows * row_bytes)
+        return fail(LKHIP_E_INVALID, "weight: %zu bytes given, %zux%zu %s needs %zu", nbytes, rows, cols,
+                    type_name(type), rows * row_bytes);
+    if (rows > 0xFFFFFFFFull || cols > 0xFFFFFFFFull) return fail(LKHIP_E_INVALID, "weight too large");
+    if (unpermute_hd && rows % unpermute_hd) return fail(LKHIP_E_INVALID, "unpermute: rows not a multiple of head_dim");
+
+    auto w = std::make_unique<lkhip_weight>();
+    w->dw.type = type;
+    w->dw.rows = (uint32_t)rows;
+    w->dw.cols = (uint32_t)cols;
+    w->bytes = (double)nbytes;
+    const uint8_t* src = (const uint8_t*)host;
+    size_t data_row = 0, aux_row = 0;
+    switch (type) {
+    case LKHIP_F32: data_row = cols * 4; break;
+    case LKHIP_F16: data_row = cols * 2; break;
+    case LKHIP_Q8_0: data_row = cols; aux_row = cols / 32 * 2; break;
+    case LKHIP_Q4_K: data_row = cols / 256 * 128; aux_row = cols / 256 * 16; break;
+    }
+    std::vector<uint8_t> hd(rows * data_row), ha(rows * aux_row);
+    auto repack = [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; r++) {
+            const uint8_t* s = src + src_row(r, unpermute_hd) * row_bytes;
+            uint8_t* d = hd.data() + r * data_row;
+            uint8_t* a = ha.data() + r * aux_row;
+            if (type == LKHIP_F32 || type == LKHIP_F16) {
+                memcpy(d, s, row_bytes);
+            } else if (type == LKHIP_Q8_0) {
+                for (size_t b = 0; b < cols / 32; b++) {
+                    memcpy(a + 2 * b, s + 34 * b, 2);
+                    memcpy(d + 32 * b, s + 34 * b + 2, 32);
+                }
+            } else {
+                for (size_t b = 0; b < cols / 256; b++) {
+                    memcpy(a + 16 * b, s + 144 * b, 16);
+                    memcpy(d + 128 * b, s + 144 * b + 16, 128);
+                }
+            }
+        }
+    };
+    const size_t nt = rows * row_bytes > (8u << 20) ? 8 : 1;
+    std::vector<std::thread> th;
+    for (size_t t = 0; t < nt; t++) th.emplace_back(repack, rows * t / nt, rows * (t + 1) / nt);
+    for (auto& t : th) t.join();
+
+    if (hipMalloc(&w->data, hd.size()) != hipSuccess)
+        return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes for a weight failed", hd.size());
+    HIP_OR_FAIL(hipMemcpy(w->data, hd.data(), hd.size(), hipMemcpyHostToDevice));
+    if (aux_row) {
+        if (hipMalloc(&w->aux, ha.size()) != hipSuccess)
+            return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes for block scales failed", ha.size());
+        HIP_OR_FAIL(hipMemcpy(w->aux, ha.data(), ha.size(), hipMemcpyHostToDevice));
+    }
+    w->dw.data = (const uint8_t*)w->data;
+    w->dw.aux = (const uint8_t*)w->aux;
+    *out = w.release();
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_weight_create(uint32_t type, size_t rows, size_t cols, const void* host, size_t nbytes,
+                                   lkhip_weight** out) {
+    if (type == LKHIP_F32) return fail(LKHIP_E_UNSUPPORTED, "F32 matrices are not a matvec weight type here");
+    return weight_create(type, rows, cols, host, nbytes, 0, out);
+}
+extern "C" void lkhip_weight_destroy(lkhip_weight* w) { delete w; }
+extern "C" double lkhip_weight_bytes(const lkhip_weight* w) { return w ? w->bytes : 0.0; }
+
+// --------------------------------------------------------------- the engine
+
+struct DevBuf {
+    void* p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p) { o.p = nullptr; }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    template <class T>
+    T* as() const { return (T*)p; }
+};
+
+static int dev_alloc(DevBuf& b, size_t bytes) {
+    if (hipMalloc(&b.p, bytes ? bytes : 4) != hipSuccess)
+        return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes failed", bytes);
+    if (hipMemset(b.p, 0, bytes ? bytes : 4) != hipSuccess) return fail(LKHIP_E_HIP, "hipMemset failed");
+    return LKHIP_OK;
+}
+
+struct Layer {
+    std::unique_ptr<lkhip_weight> q, k, v, o, gate, up, down;
+    DevBuf in_norm, post_norm, bq, bk, bv;
+    bool has_bias = false;
+};
+
+struct lkhip_engine {
+    lkhip_config cfg{};
+    uint32_t hd = 0, qd = 0, kvd = 0;
+    std::vector<Layer> layers;
+    std::unique_ptr<lkhip_weight> embed, lm_head_own;
+    lkhip_weight* lm_head = nullptr;
+    DevBuf norm;
+    LkFreq freq{};
+    double matvec_bytes = 0;
+    int device = 0;
+};
+
+struct Named {
+    const lkhip_tensor* t = nullptr;
+};
+
+static int upload_vec(DevBuf& b, const lkhip_tensor* t, size_t n, const char* what) {
+    if (!t) return fail(LKHIP_E_INVALID, "missing tensor %s", what);
+    size_t cnt = t->n_dims == 2 ? t->dims[0] * t->dims[1] : t->dims[0];
+    if (cnt != n) return fail(LKHIP_E_INVALID, "%s has %zu values but the config implies %zu", t->name, cnt, n);
+    std::vector<float> h(n);
+    if (t->ggml_type == LKHIP_F32) {
+        if (t->nbytes != n * 4) return fail(LKHIP_E_INVALID, "%s: byte size mismatch", t->name);
+        memcpy(h.data(), t->data, n * 4);
+    } else if (t->ggml_type == LKHIP_F16) {
+        if (t->nbytes != n * 2) return fail(LKHIP_E_INVALID, "%s: byte size mismatch", t->name);
+        const uint16_t* s = (const uint16_t*)t->data;
+        for (size_t i = 0; i < n; i++) {
+            // exact f16 -> f32
+            uint32_t hbits = s[i], sign = (hbits >> 15) << 31, e = (hbits >> 10) & 31, m = hbits & 1023, bits;
+            if (e == 0) {
+                if (m == 0) bits = sign;
+                else {
+                    int k = -1;
+                    do { m <<= 1; k++; } while (!(m & 1024));
+                    bits = sign | ((uint32_t)(112 - k) << 23) | ((m & 1023) << 13);
+                }
+            } else if (e == 31) bits = sign | 0x7f800000u | (m << 13);
+            else bits = sign | ((e + 112) << 23) | (m << 13);
+            memcpy(&h[i], &bits, 4);
+        }
+    } else {
+        return fail(LKHIP_E_UNSUPPORTED, "%s: norm/bias tensors must be F32 or F16, got %s", t->name,
+                    type_name(t->ggml_type));
+    }
+    int rc = dev_alloc(b, n * 4);
+    if (rc) return rc;
+    HIP_OR_FAIL(hipMemcpy(b.p, h.data(), n * 4, hipMemcpyHostToDevice));
+    return LKHIP_OK;
+}
+
+static int upload_mat(std::unique_ptr<lkhip_weight>& w, const lkhip_tensor* t, size_t rows, size_t cols,
+                      size_t unpermute_hd, const char* what) {
+    if (!t) return fail(LKHIP_E_INVALID, "missing tensor %s", what);
+    if (t->n_dims != 2 || t->dims[0] != rows || t->dims[1] != cols)
+        return fail(LKHIP_E_INVALID, "%s is %llux%llu but the config implies %zux%zu", t->name,
+                    (unsigned long long)t->dims[0], (unsigned long long)(t->n_dims == 2 ? t->dims[1] : 0), rows,
+                    cols);
+    lkhip_weight* p = nullptr;
+    int rc = weight_create(t->ggml_type, rows, cols, t->data, t->nbytes, unpermute_hd, &p);
+    if (rc) {
+        std::string why = g_err;
+        return fail(rc, "%s: %s", t->name, why.c_str());
+    }
+    w.reset(p);
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_tensor* tensors, size_t n_tensors,
+                                           int llama_permuted, lkhip_engine** out) {
+    if (!cfg || !out || (!tensors && n_tensors)) return fail(LKHIP_E_INVALID, "engine: null argument");
+    *out = nullptr;
+    if (lkhip_device_count() == 0) return fail(LKHIP_E_HIP, "no HIP device visible — the hip backend needs an AMD GPU");
+    auto e = std::make_unique<lkhip_engine>();
+    e->cfg = *cfg;
+    if (!cfg->num_attention_heads || !cfg->num_key_value_heads || !cfg->hidden_size || !cfg->num_hidden_layers ||
+        !cfg->vocab_size || !cfg->intermediate_size)
+        return fail(LKHIP_E_INVALID, "engine: config has a zero dimension");
+    e->hd = cfg->head_dim ? cfg->head_dim : cfg->hidden_size / cfg->num_attention_heads;
+    if (e->hd != 64)
+        return fail(LKHIP_E_UNSUPPORTED, "head_dim %u is not supported by the hip backend — 64 only", e->hd);
+    if (cfg->num_attention_heads % cfg->num_key_value_heads ||
+        cfg->num_attention_heads / cfg->num_key_value_heads > 8)
+        return fail(LKHIP_E_UNSUPPORTED, "GQA group %u/%u is not supported — query heads per kv head must be 1..8",
+                    cfg->num_attention_heads, cfg->num_key_value_heads);
+    e->qd = cfg->num_attention_heads * e->hd;
+    e->kvd = cfg->num_key_value_heads * e->hd;
+    (void)hipGetDevice(&e->device);
+    // RoPE inverse frequencies with the CPU path's own f32 powf (src/model.rs:273).
+    for (uint32_t i = 0; i < e->hd / 2; i++)
+        e->freq.f[i] = powf(cfg->rope_theta, -(2.0f * (float)i) / (float)e->hd);
+
+    auto find = [&](const std::string& name) -> const lkhip_tensor* {
+        for (size_t i = 0; i < n_tensors; i++)
+            if (tensors[i].name && name == tensors[i].name) return &tensors[i];
+        return nullptr;
+    };
+    const size_t h = cfg->hidden_size, I = cfg->intermediate_size;
+    const size_t uhd = llama_permuted ? e->hd : 0;
+    e->layers.resize(cfg->num_hidden_layers);
+    int rc;
+    uint32_t mv_type = 0;
+    for (uint32_t L = 0; L < cfg->num_hidden_layers; L++) {
+        Layer& ly = e->layers[L];
+        std::string p = "model.layers." + std::to_string(L) + ".";
+        if ((rc = upload_vec(ly.in_norm, find(p + "input_layernorm.weight"), h, (p + "input_layernorm.weight").c_str())))
+            return rc;
+        if ((rc = upload_vec(ly.post_norm, find(p + "post_attention_layernorm.weight"), h,
+                             (p + "post_attention_layernorm.weight").c_str())))
+            return rc;
+        if ((rc = upload_mat(ly.q, find(p + "self_attn.q_proj.weight"), e->qd, h, uhd, "q_proj"))) return rc;
+        if ((rc = upload_mat(ly.k, find(p + "self_attn.k_proj.weight"), e->kvd, h, uhd, "k_proj"))) return rc;
+        if ((rc = upload_mat(ly.v, find(p + "self_attn.v_proj.weight"), e->kvd, h, 0, "v_proj"))) return rc;
+        if ((rc = upload_mat(ly.o, find(p + "self_attn.o_proj.weight"), h, e->qd, 0, "o_proj"))) return rc;
+        if ((rc = upload_mat(ly.gate, find(p + "mlp.gate_proj.weight"), I, h, 0, "gate_proj"))) return rc;
+        if ((rc = upload_mat(ly.up, find(p + "mlp.up_proj.weight"), I, h, 0, "up_proj"))) return rc;
+        if ((rc = upload_mat(ly.down, find(p + "mlp.down_proj.weight"), h, I, 0, "down_proj"))) return rc;
+        const lkhip_tensor* bq = find(p + "self_attn.q_proj.bias");
+        const lkhip_tensor* bk = find(p + "self_attn.k_proj.bias");
+        const lkhip_tensor* bv = find(p + "self_attn.v_proj.bias");
+        if (bq || bk || bv) {
+            // Qwen2 carries all three (model.rs reads each independently; a
+            // missing one is zero here, which is what no-bias means).
+            std::vector<float> zero(std::max(e->qd, e->kvd), 0.f);
+            lkhip_tensor zq{"zero", LKHIP_F32, 1, {e->qd, 0}, zero.data(), (uint64_t)e->qd * 4};
+            lkhip_tensor zk{"zero", LKHIP_F32, 1, {e->kvd, 0}, zero.data(), (uint64_t)e->kvd * 4};
+            if ((rc = upload_vec(ly.bq, bq ? bq : &zq, e->qd, "q bias"))) return rc;
+            if ((rc = upload_vec(ly.bk, bk ? bk : &zk, e->kvd, "k bias"))) return rc;
+            if ((rc = upload_vec(ly.bv, bv ? bv : &zk, e->kvd, "v bias"))) return rc;
+            ly.has_bias = true;
+        }
+        const uint32_t t = ly.q->dw.type;
+        if (ly.k->dw.type != t || ly.v->dw.type != t)
+            return fail(LKHIP_E_UNSUPPORTED, "layer %u: q/k/v weights must share one type for the fused QKV matvec", L);
+        if (ly.gate->dw.type != ly.up->dw.type)
+            return fail(LKHIP_E_UNSUPPORTED, "layer %u: gate/up weights must share one type for the fused SwiGLU matvec",
+                        L);
+        mv_type = t;
+        for (auto* w : {ly.q.get(), ly.k.get(), ly.v.get(), ly.o.get(), ly.gate.get(), ly.up.get(), ly.down.get()})
+            e->matvec_bytes += w->bytes;
+    }
+    (void)mv_type;
+    if ((rc = upload_mat(e->embed, find("model.embed_tokens.weight"), cfg->vocab_size, h, 0, "embed_tokens")))
+        return rc;
+    if ((rc = upload_vec(e->norm, find("model.norm.weight"), h, "model.norm.weight"))) return rc;
+    if (const lkhip_tensor* lm = find("lm_head.weight")) {
+        if ((rc = upload_mat(e->lm_head_own, lm, cfg->vocab_size, h, 0, "lm_head"))) return rc;
+        e->lm_head = e->lm_head_own.get();
+    } else {
+        e->lm_head = e->embed.get();  // tied (src/model.rs:181-186)
+    }
+    if (e->lm_head->dw.type == LKHIP_F32)
+        return fail(LKHIP_E_UNSUPPORTED, "lm_head must be F16, Q8_0 or Q4_K on the hip backend");
+    e->matvec_bytes += e->lm_head->bytes;
+    *out = e.release();
+    return LKHIP_OK;
+}
+
+extern "C" void lkhip_engine_destroy(lkhip_engine* e) { delete e; }
+extern "C" int lkhip_engine_config(const lkhip_engine* e, lkhip_config* out) {
+    if (!e || !out) return fail(LKHIP_E_INVALID, "null argument");
+    *out = e->cfg;
+    out->head_dim = e->hd;
+    return LKHIP_OK;
+}
+extern "C" double lkhip_engine_matvec_bytes(const lkhip_engine* e) { return e ? e->matvec_bytes : 0.0; }
+
+// -------------------------------------------------------------- sessions
+
+enum Cat { C_MATVEC = 0, C_LMHEAD = 1, C_ATTN = 2, C_OTHER = 3 };
+
+struct lkhip_session {
+    lkhip_engine* e = nullptr;
+    size_t max_seq = 0;
+    hipStream_t stream = nullptr;
+    DevBuf kc, vc;  // [layer][n_kv][max_seq][64] f16
+    DevBuf x, xn, qkv, att, inner, logits, part, keys, state, feed, ids_out;
+    LkStepState* h_state = nullptr;  // pinned
+    float* h_logits = nullptr;       // pinned
+    uint32_t n_keys = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    // profiling
+    bool profiling = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<int> ev_cat;
+    std::vector<double> ev_bytes;
+    lkhip_profile prof{};
+    ~lkhip_session() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        for (auto v : ev) (void)hipEventDestroy(v);
+        if (h_state) (void)hipHostFree(h_state);
+        if (h_logits) (void)hipHostFree(h_logits);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+static size_t kv_layer_elems(const lkhip_session* s) {
+    return (size_t)s->e->cfg.num_key_value_heads * s->max_seq * 64;
+}
+
+// Records one launch for profiling: an event after every launch.
+struct Rec {
+    lkhip_session* s;
+    int idx = 0;
+    explicit Rec(lkhip_session* s_) : s(s_) {}
+    hipError_t mark(int cat, double bytes) {
+        if (!s->profiling) return hipSuccess;
+        if ((size_t)idx + 1 >= s->ev.size()) return hipErrorInvalidValue;
+        s->ev_cat[idx] = cat;
+        s->ev_bytes[idx] = bytes;
+        idx++;
+        return hipEventRecord(s->ev[idx], s->stream);
+    }
+};
+
+static LkMvArgs mv_args(const float* x, uint32_t cols) {
+    LkMvArgs a{};
+    a.x = x;
+    a.cols = cols;
+    return a;
+}
+
+// The whole decode step of one token (Model::forward, src/model.rs:196-262)
+// enqueued on the session stream; reads token/pos from the device state.
+static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
+    lkhip_engine* e = s->e;
+    const lkhip_config& c = e->cfg;
+    hipStream_t st = s->stream;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size;
+    float* x = s->x.as<float>();
+    float* xn = s->xn.as<float>();
+    float* qkv = s->qkv.as<float>();
+    LkStepState* state = s->state.as<LkStepState>();
+    hipError_t err;
+#define STEP(call, cat, bytes)                   \
+    do {                                         \
+        if ((err = (call)) != hipSuccess) return err; \
+        if ((err = rec.mark(cat, bytes)) != hipSuccess) return err; \
+    } while (0)
+
+    STEP(lk_embed_step_launch(e->embed->dw, state, x, st), C_OTHER, 0);
+    for (uint32_t L = 0; L < c.num_hidden_layers; L++) {
+        Layer& ly = e->layers[L];
+        STEP(lk_rmsnorm_launch(x, ly.in_norm.as<float>(), 1, h, c.rms_norm_eps, xn, st), C_OTHER, 0);
+        {
+            LkMvArgs a = mv_args(xn, h);
+            a.nseg = 3;
+            a.seg[0] = {ly.q->dw, ly.has_bias ? ly.bq.as<float>() : nullptr, qkv};
+            a.seg[1] = {ly.k->dw, ly.has_bias ? ly.bk.as<float>() : nullptr, qkv + e->qd};
+            a.seg[2] = {ly.v->dw, ly.has_bias ? ly.bv.as<float>() : nullptr, qkv + e->qd + e->kvd};
+            a.total_rows = e->qd + 2 * e->kvd;
+            STEP(lk_matvec_launch(a, LK_MV_STORE, st), C_MATVEC, ly.q->bytes + ly.k->bytes + ly.v->bytes);
+        }
+        uint16_t* kc = s->kc.as<uint16_t>() + (size_t)L * kv_layer_elems(s);
+        uint16_t* vc = s->vc.as<uint16_t>() + (size_t)L * kv_layer_elems(s);
+        STEP(lk_rope_kv_launch(qkv, c.num_attention_heads, c.num_key_value_heads, e->freq, state, nullptr, 1, kc, vc,
+                               (uint32_t)s->max_seq, 0, nullptr, st),
+             C_OTHER, 0);
+        {
+            LkAttnArgs a{};
+            a.q = qkv;
+            a.k = kc;
+            a.v = vc;
+            a.out = s->att.as<float>();
+            a.part = s->part.as<float>();
+            a.st = state;
+            a.n_seq = 1;
+            a.n_heads = c.num_attention_heads;
+            a.n_kv = c.num_key_value_heads;
+            a.max_seq = (uint32_t)s->max_seq;
+            a.seq_stride = 0;
+            a.q_stride = e->qd;
+            STEP(lk_attn_launch(a, st), C_ATTN, 0);
+        }
+        {
+            LkMvArgs a = mv_args(s->att.as<float>(), e->qd);
+            a.nseg = 1;
+            a.seg[0] = {ly.o->dw, nullptr, x};
+            a.total_rows = h;
+            STEP(lk_matvec_launch(a, LK_MV_ACC, st), C_MATVEC, ly.o->bytes);
+        }
+        STEP(lk_rmsnorm_launch(x, ly.post_norm.as<float>(), 1, h, c.rms_norm_eps, xn, st), C_OTHER, 0);
+        {
+            LkMvArgs a = mv_args(xn, h);
+            a.nseg = 2;
+            a.seg[0] = {ly.gate->dw, nullptr, s->inner.as<float>()};
+            a.seg[1] = {ly.up->dw, nullptr, nullptr};
+            a.total_rows = I;
+            STEP(lk_matvec_launch(a, LK_MV_SWIGLU, st), C_MATVEC, ly.gate->bytes + ly.up->bytes);
+        }
+        {
+            LkMvArgs a = mv_args(s->inner.as<float>(), I);
+            a.nseg = 1;
+            a.seg[0] = {ly.down->dw, nullptr, x};
+            a.total_rows = h;
+            STEP(lk_matvec_launch(a, LK_MV_ACC, st), C_MATVEC, ly.down->bytes);
+        }
+    }
+    STEP(lk_rmsnorm_launch(x, e->norm.as<float>(), 1, h, c.rms_norm_eps, xn, st), C_OTHER, 0);
+    {
+        LkMvArgs a = mv_args(xn, h);
+        a.nseg = 1;
+        a.seg[0] = {e->lm_head->dw, nullptr, s->logits.as<float>()};
+        a.total_rows = c.vocab_size;
+        a.keys = s->keys.as<uint64_t>();
+        STEP(lk_matvec_launch(a, LK_MV_ARGMAX, st), C_LMHEAD, e->lm_head->bytes);
+    }
+    STEP(lk_step_finish_launch(s->keys.as<uint64_t>(), s->n_keys, state, s->feed.as<uint32_t>(),
+                               s->ids_out.as<uint32_t>(), st),
+         C_OTHER, 0);
+#undef STEP
+    return hipSuccess;
+}
+
+static int build_graph(lkhip_session* s) {
+    Rec rec(s);
+    HIP_OR_FAIL(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+    hipError_t e1 = enqueue_step(s, rec);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(s->stream, &g);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(LKHIP_E_HIP, "capturing the decode step failed: %s",
+                    hipGetErrorString(e1 != hipSuccess ? e1 : e2));
+    }
+    s->graph = g;
+    HIP_OR_FAIL(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_session** out) {
+    if (!e || !out) return fail(LKHIP_E_INVALID, "session: null argument");
+    *out = nullptr;
+    if (max_seq == 0 || max_seq > 0x7FFFFFFF) return fail(LKHIP_E_INVALID, "session: max_seq must be in 1..2^31");
+    (void)hipSetDevice(e->device);
+    auto s = std::make_unique<lkhip_session>();
+    s->e = e;
+    s->max_seq = max_seq;
+    const lkhip_config& c = e->cfg;
+    HIP_OR_FAIL(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    int rc;
+    const size_t kv = (size_t)c.num_hidden_layers * kv_layer_elems(s.get()) * 2;
+    if ((rc = dev_alloc(s->kc, kv)) || (rc = dev_alloc(s->vc, kv))) return rc;
+    if ((rc = dev_alloc(s->x, c.hidden_size * 4)) || (rc = dev_alloc(s->xn, c.hidden_size * 4)) ||
+        (rc = dev_alloc(s->qkv, (e->qd + 2 * e->kvd) * 4)) || (rc = dev_alloc(s->att, e->qd * 4)) ||
+        (rc = dev_alloc(s->inner, (size_t)c.intermediate_size * 4)) ||
+        (rc = dev_alloc(s->logits, (size_t)c.vocab_size * 4)))
+        return rc;
+    if ((rc = dev_alloc(s->part, lk_attn_part_floats(1, c.num_attention_heads, (uint32_t)max_seq) * 4))) return rc;
+    s->n_keys = lk_matvec_plan(e->lm_head->dw.type, c.vocab_size, c.hidden_size, LK_MV_ARGMAX).blocks;
+    if ((rc = dev_alloc(s->keys, (size_t)s->n_keys * 8))) return rc;
+    if ((rc = dev_alloc(s->state, sizeof(LkStepState)))) return rc;
+    if ((rc = dev_alloc(s->feed, max_seq * 4)) || (rc = dev_alloc(s->ids_out, max_seq * 4))) return rc;
+    HIP_OR_FAIL(hipHostMalloc((void**)&s->h_state, sizeof(LkStepState), hipHostMallocDefault));
+    HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
+    if ((rc = build_graph(s.get()))) return rc;
+    *out = s.release();
+    return LKHIP_OK;
+}
+
+extern "C" void lkhip_session_destroy(lkhip_session* s) {
+    if (s && s->stream) (void)hipStreamSynchronize(s->stream);
+    delete s;
+}
+
+static int set_state(lkhip_session* s, uint32_t token, size_t pos, uint32_t n_feed) {
+    memset(s->h_state, 0, sizeof(LkStepState));
+    s->h_state->token = token;
+    s->h_state->pos = (uint32_t)pos;
+    s->h_state->n_feed = n_feed;
+    HIP_OR_FAIL(hipMemcpyAsync(s->state.p, s->h_state, sizeof(LkStepState), hipMemcpyHostToDevice, s->stream));
+    return LKHIP_OK;
+}
+
+// Runs one step: graph replay, or eager with events when profiling.
+static int run_step(lkhip_session* s) {
+    if (!s->profiling) {
+        HIP_OR_FAIL(hipGraphLaunch(s->exec, s->stream));
+        return LKHIP_OK;
+    }
+    Rec rec(s);
+    HIP_OR_FAIL(hipEventRecord(s->ev[0], s->stream));
+    hipError_t err = enqueue_step(s, rec);
+    if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
+    HIP_OR_FAIL(hipEventSynchronize(s->ev[rec.idx]));
+    for (int i = 0; i < rec.idx; i++) {
+        float ms = 0.f;
+        HIP_OR_FAIL(hipEventElapsedTime(&ms, s->ev[i], s->ev[i + 1]));
+        switch (s->ev_cat[i]) {
+        case C_MATVEC:
+            s->prof.matvec_launches++;
+            s->prof.matvec_ms += ms;
+            s->prof.matvec_bytes += s->ev_bytes[i];
+            break;
+        case C_LMHEAD:
+            s->prof.lm_head_launches++;
+            s->prof.lm_head_ms += ms;
+            s->prof.lm_head_bytes += s->ev_bytes[i];
+            s->prof.matvec_launches++;
+            s->prof.matvec_ms += ms;
+            s->prof.matvec_bytes += s->ev_bytes[i];
+            break;
+        case C_ATTN: s->prof.attn_ms += ms; break;
+        default: s->prof.other_ms += ms; break;
+        }
+    }
+    s->prof.tokens++;
+    return LKHIP_OK;
+}
+
+static int check_tok(lkhip_session* s, uint32_t token, size_t pos) {
+    if (token >= s->e->cfg.vocab_size)
+        return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", token, s->e->cfg.vocab_size);
+    if (pos >= s->max_seq)
+        return fail(LKHIP_E_INVALID, "position %zu exceeds the session's KV cache (%zu positions)", pos, s->max_seq);
+    return LKHIP_OK;
+}
+
+static int copy_logits(lkhip_session* s, float* out) {
+    const size_t n = s->e->cfg.vocab_size;
+    HIP_OR_FAIL(hipMemcpyAsync(s->h_logits, s->logits.p, n * 4, hipMemcpyDeviceToHost, s->stream));
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    memcpy(out, s->h_logits, n * 4);
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_forward(lkhip_session* s, uint32_t token, size_t pos, float* logits_out) {
+    if (!s || !logits_out) return fail(LKHIP_E_INVALID, "forward: null argument");
+    int rc;
+    if ((rc = check_tok(s, token, pos)) || (rc = set_state(s, token, pos, 0)) || (rc = run_step(s))) return rc;
+    return copy_logits(s, logits_out);
+}
+
+extern "C" int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size_t n, float* logits_out) {
+    if (!s || (!ids && n)) return fail(LKHIP_E_INVALID, "prefill: null argument");
+    if (n == 0) return fail(LKHIP_E_INVALID, "empty prompt");
+    if (n > s->max_seq)
+        return fail(LKHIP_E_INVALID, "prompt (%zu tokens) exceeds the session's context (%zu)", n, s->max_seq);
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= s->e->cfg.vocab_size)
+            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", ids[i], s->e->cfg.vocab_size);
+    int rc;
+    if (n > 1) HIP_OR_FAIL(hipMemcpyAsync(s->feed.p, ids + 1, (n - 1) * 4, hipMemcpyHostToDevice, s->stream));
+    if ((rc = set_state(s, ids[0], 0, (uint32_t)(n - 1)))) return rc;
+    for (size_t i = 0; i < n; i++)
+        if ((rc = run_step(s))) return rc;
+    if (logits_out) return copy_logits(s, logits_out);
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n, size_t pos0,
+                                           float* logits_out) {
+    if (!s || !ids || !logits_out) return fail(LKHIP_E_INVALID, "forward_batch: null argument");
+    for (size_t i = 0; i < n; i++) {
+        int rc = lkhip_session_forward(s, ids[i], pos0 + i, logits_out + i * (size_t)s->e->cfg.vocab_size);
+        if (rc) return rc;
+    }
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, size_t pos, size_t n_steps,
+                                           uint32_t* ids_out, float* logits_last) {
+    if (!s || (!ids_out && n_steps)) return fail(LKHIP_E_INVALID, "decode_greedy: null argument");
+    if (n_steps == 0) return LKHIP_OK;
+    int rc;
+    if ((rc = check_tok(s, token, pos))) return rc;
+    if (pos + n_steps > s->max_seq)
+        return fail(LKHIP_E_INVALID, "decode of %zu steps from position %zu exceeds the session's context (%zu)",
+                    n_steps, pos, s->max_seq);
+    if ((rc = set_state(s, token, pos, 0))) return rc;
+    for (size_t i = 0; i < n_steps; i++)
+        if ((rc = run_step(s))) return rc;
+    HIP_OR_FAIL(hipMemcpyAsync(s->h_logits, s->ids_out.p, n_steps * 4, hipMemcpyDeviceToHost, s->stream));
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    memcpy(ids_out, s->h_logits, n_steps * 4);
+    if (logits_last) return copy_logits(s, logits_last);
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int which_v, float* out) {
+    if (!s || !out) return fail(LKHIP_E_INVALID, "read_kv: null argument");
+    const lkhip_config& c = s->e->cfg;
+    if (layer >= c.num_hidden_layers || pos >= s->max_seq) return fail(LKHIP_E_INVALID, "read_kv: out of range");
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    const uint16_t* base = (which_v ? s->vc : s->kc).as<uint16_t>() + (size_t)layer * kv_layer_elems(s);
+    std::vector<uint16_t> h(64);
+    for (uint32_t kh = 0; kh < c.num_key_value_heads; kh++) {
+        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->max_seq + pos) * 64, 128, hipMemcpyDeviceToHost));
+        for (int d = 0; d < 64; d++) {
+            uint32_t hb = h[d], sign = (hb >> 15) << 31, ex = (hb >> 10) & 31, m = hb & 1023, bits;
+            if (ex == 0) {
+                if (m == 0) bits = sign;
+                else {
+                    int k = -1;
+                    do { m <<= 1; k++; } while (!(m & 1024));
+                    bits = sign | ((uint32_t)(112 - k) << 23) | ((m & 1023) << 13);
+                }
+            } else if (ex == 31) bits = sign | 0x7f800000u | (m << 13);
+            else bits = sign | ((ex + 112) << 23) | (m << 13);
+            memcpy(&out[kh * 64 + d], &bits, 4);
+        }
+    }
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_set_profiling(lkhip_session* s, int on) {
+    if (!s) return fail(LKHIP_E_INVALID, "null session");
+    s->profiling = on != 0;
+    if (s->profiling && s->ev.empty()) {
+        const size_t n = 16 + (size_t)s->e->cfg.num_hidden_layers * 12;
+        s->ev.resize(n);
+        s->ev_cat.resize(n);
+        s->ev_bytes.resize(n);
+        for (auto& v : s->ev) HIP_OR_FAIL(hipEventCreate(&v));
+    }
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_profile(lkhip_session* s, lkhip_profile* out, int reset) {
+    if (!s || !out) return fail(LKHIP_E_INVALID, "null argument");
+    *out = s->prof;
+    if (reset) s->prof = lkhip_profile{};
+    return LKHIP_OK;
+}
+
+// ------------------------------------------------------------------ batcher
+// Continuous batching seam (src/engine.rs:42-47).  One session per slot; a
+// decode step advances each row through its slot's session.
+
+struct lkhip_batch {
+    lkhip_engine* e = nullptr;
+    std::vector<lkhip_session*> slots;
+    ~lkhip_batch() {
+        for (auto* s : slots) lkhip_session_destroy(s);
+    }
+};
+
+extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_seq, lkhip_batch** out) {
+    if (!e || !out || n_slots == 0) return fail(LKHIP_E_INVALID, "batch: bad argument");
+    *out = nullptr;
+    auto b = std::make_unique<lkhip_batch>();
+    b->e = e;
+    for (size_t i = 0; i < n_slots; i++) {
+        lkhip_session* s = nullptr;
+        int rc = lkhip_session_create(e, max_seq, &s);
+        if (rc) return rc;
+        b->slots.push_back(s);
+    }
+    *out = b.release();
+    return LKHIP_OK;
+}
+extern "C" void lkhip_batch_destroy(lkhip_batch* b) { delete b; }
+extern "C" int lkhip_batch_prefill(lkhip_batch* b, uint32_t slot, const uint32_t* ids, size_t n, float* logits_out) {
+    if (!b || slot >= b->slots.size()) return fail(LKHIP_E_INVALID, "batch prefill: slot out of range");
+    return lkhip_session_prefill(b->slots[slot], ids, n, logits_out);
+}
+extern "C" int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, float* logits_out) {
+    if (!b || (!rows && n_rows) || (!logits_out && n_rows)) return fail(LKHIP_E_INVALID, "decode_step: null argument");
+    for (size_t i = 0; i < n_rows; i++) {
+        if (rows[i].slot >= b->slots.size()) return fail(LKHIP_E_INVALID, "decode_step: slot %u out of range", rows[i].slot);
+        for (size_t j = 0; j < i; j++)
+            if (rows[j].slot == rows[i].slot)
+                return fail(LKHIP_E_INVALID, "decode_step: slot %u appears twice in one step", rows[i].slot);
+    }
+    for (size_t i = 0; i < n_rows; i++) {
+        int rc = lkhip_session_forward(b->slots[rows[i].slot], rows[i].token, rows[i].pos,
+                                       logits_out + i * (size_t)b->e->cfg.vocab_size);
+        if (rc) return rc;
+    }
+    return LKHIP_OK;
+}
+
+// ------------------------------------------------------------------ memory
+
+extern "C" int lkhip_malloc(void** p, size_t bytes) {
+    if (!p) return fail(LKHIP_E_INVALID, "null argument");
+    if (hipMalloc(p, bytes ? bytes : 4) != hipSuccess) return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes failed", bytes);
+    return LKHIP_OK;
+}
+extern "C" int lkhip_free(void* p) {
+    HIP_OR_FAIL(hipFree(p));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    HIP_OR_FAIL(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    HIP_OR_FAIL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_memset(void* p, int v, size_t bytes) {
+    HIP_OR_FAIL(hipMemset(p, v, bytes));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_synchronize(void) {
+    HIP_OR_FAIL(hipDeviceSynchronize());
+    return LKHIP_OK;
+}
+extern "C" int lkhip_stream_create(void** s) {
+    if (!s) return fail(LKHIP_E_INVALID, "null argument");
+    HIP_OR_FAIL(hipStreamCreateWithFlags((hipStream_t*)s, hipStreamNonBlocking));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_stream_destroy(void* s) {
+    HIP_OR_FAIL(hipStreamDestroy((hipStream_t)s));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_stream_synchronize(void* s) {
+    HIP_OR_FAIL(hipStreamSynchronize((hipStream_t)s));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_event_create(void** ev) {
+    if (!ev) return fail(LKHIP_E_INVALID, "null argument");
+    HIP_OR_FAIL(hipEventCreate((hipEvent_t*)ev));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_event_destroy(void* ev) {
+    HIP_OR_FAIL(hipEventDestroy((hipEvent_t)ev));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_event_record(void* ev, void* st) {
+    HIP_OR_FAIL(hipEventRecord((hipEvent_t)ev, (hipStream_t)st));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_event_elapsed_ms(void* a, void* b, float* ms) {
+    if (!ms) return fail(LKHIP_E_INVALID, "null argument");
+    HIP_OR_FAIL(hipEventSynchronize((hipEvent_t)b));
+    HIP_OR_FAIL(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return LKHIP_OK;
+}
+
+// ------------------------------------------------------------------ kernels
+
+#define LAUNCH_OR_FAIL(expr)                                                                                  \
+    do {                                                                                                      \
+        hipError_t _e = (expr);                                                                               \
+        if (_e != hipSuccess) return fail(LKHIP_E_HIP, "kernel launch failed: %s", hipGetErrorString(_e));   \
+    } while (0)
+
+extern "C" int lkhip_dequant_rows(const lkhip_weight* w, size_t row0, size_t n_rows, float* out, void* stream) {
+    if (!w || (!out && n_rows)) return fail(LKHIP_E_INVALID, "dequant_rows: null argument");
+    if (row0 + n_rows > w->dw.rows) return fail(LKHIP_E_INVALID, "dequant_rows: rows out of range");
+    LAUNCH_OR_FAIL(lk_dequant_launch(w->dw, (uint32_t)row0, (uint32_t)n_rows, out, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
+                            void* stream) {
+    if (!w || !x || !y) return fail(LKHIP_E_INVALID, "matvec: null argument");
+    LkMvArgs a = mv_args(x, w->dw.cols);
+    a.nseg = 1;
+    a.seg[0] = {w->dw, bias, y};
+    a.total_rows = w->dw.rows;
+    LAUNCH_OR_FAIL(lk_matvec_launch(a, accumulate ? LK_MV_ACC : LK_MV_STORE, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+extern "C" int lkhip_q8_0_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
+                                 void* stream) {
+    if (w && w->dw.type != LKHIP_Q8_0) return fail(LKHIP_E_INVALID, "q8_0_matvec: weight is %s", type_name(w->dw.type));
+    return lkhip_matvec(w, x, bias, y, accumulate, stream);
+}
+extern "C" int lkhip_q4_k_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
+                                 void* stream) {
+    if (w && w->dw.type != LKHIP_Q4_K) return fail(LKHIP_E_INVALID, "q4_k_matvec: weight is %s", type_name(w->dw.type));
+    return lkhip_matvec(w, x, bias, y, accumulate, stream);
+}
+
+extern "C" int lkhip_rmsnorm(const float* x, const float* w, size_t n_rows, size_t n, float eps, float* y,
+                             void* stream) {
+    if ((!x || !w || !y) && n_rows) return fail(LKHIP_E_INVALID, "rmsnorm: null argument");
+    if (n == 0) return fail(LKHIP_E_INVALID, "rmsnorm: empty row");
+    LAUNCH_OR_FAIL(lk_rmsnorm_launch(x, w, (uint32_t)n_rows, (uint32_t)n, eps, y, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_rope_pairs(float* x, size_t n_rows, size_t n, size_t head_dim, const uint32_t* pos, float theta,
+                                void* stream) {
+    if ((!x || !pos) && n_rows) return fail(LKHIP_E_INVALID, "rope: null argument");
+    if (head_dim == 0 || head_dim % 2 || head_dim > 128 || n % head_dim)
+        return fail(LKHIP_E_INVALID, "rope: n (%zu) must be a multiple of an even head_dim <= 128 (%zu)", n, head_dim);
+    LkFreq f{};
+    for (size_t i = 0; i < head_dim / 2; i++) f.f[i] = powf(theta, -(2.0f * (float)i) / (float)head_dim);
+    LAUNCH_OR_FAIL(lk_rope_launch(x, (uint32_t)n_rows, (uint32_t)n, (uint32_t)head_dim, pos, f, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_swiglu(const float* g, const float* u, size_t n, float* out, void* stream) {
+    if ((!g || !u || !out) && n) return fail(LKHIP_E_INVALID, "swiglu: null argument");
+    LAUNCH_OR_FAIL(lk_swiglu_launch(g, u, (uint32_t)n, out, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_embed_gather(const lkhip_weight* table, const uint32_t* ids, size_t n_ids, float* out,
+                                  void* stream) {
+    if (!table || ((!ids || !out) && n_ids)) return fail(LKHIP_E_INVALID, "embed_gather: null argument");
+    LAUNCH_OR_FAIL(lk_gather_launch(table->dw, ids, (uint32_t)n_ids, out, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                 const uint32_t* ctx_len, size_t n_seq, size_t n_heads, size_t n_kv_heads,
+                                 size_t head_dim, size_t max_seq, float* out, void* stream) {
+    if (!q || !k_cache || !v_cache || !ctx_len || !out) return fail(LKHIP_E_INVALID, "attn_decode: null argument");
+    if (head_dim != 64) return fail(LKHIP_E_UNSUPPORTED, "attn_decode: head_dim %zu — 64 only", head_dim);
+    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
+        return fail(LKHIP_E_UNSUPPORTED, "attn_decode: GQA group %zu/%zu not supported (1..8)", n_heads, n_kv_heads);
+    if (n_seq == 0 || max_seq == 0) return LKHIP_OK;
+    // Partial buffer for this call, cached per thread and grown on demand.
+    // (Deliberately never freed at thread exit: the HIP runtime may already be
+    // torn down by then.)
+    static thread_local void* part = nullptr;
+    static thread_local size_t part_bytes = 0;
+    const size_t need = lk_attn_part_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq) * 4;
+    if (need > part_bytes) {
+        HIP_OR_FAIL(hipStreamSynchronize((hipStream_t)stream));
+        if (part) (void)hipFree(part);
+        part = nullptr;
+        part_bytes = 0;
+        if (hipMalloc(&part, need) != hipSuccess) {
+            part = nullptr;
+            return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes failed", need);
+        }
+        part_bytes = need;
+    }
+    LkAttnArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.part = (float*)part;
+    a.ctx_len = ctx_len;
+    a.n_seq = (uint32_t)n_seq;
+    a.n_heads = (uint32_t)n_heads;
+    a.n_kv = (uint32_t)n_kv_heads;
+    a.max_seq = (uint32_t)max_seq;
+    a.seq_stride = (uint64_t)n_kv_heads * max_seq * 64;
+    a.q_stride = n_heads * 64;
+    LAUNCH_OR_FAIL(lk_attn_launch(a, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream) {
+    if ((!x || !out) && n_rows) return fail(LKHIP_E_INVALID, "argmax: null argument");
+    LAUNCH_OR_FAIL(lk_argmax_rows_launch(x, (uint32_t)n_rows, (uint32_t)n, out, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_engine_create_gguf(const char* path, lkhip_engine** out) {
+    (void)path;
+    if (out) *out = nullptr;
+    return fail(LKHIP_E_UNSUPPORTED, "GGUF file loading is not wired yet — build the engine from tensors "
+                                     "(lkhip_engine_create_tensors)");
+}

@@ -1,0 +1,207 @@
+// layer.hip -- the small fused layer kernels of the decode step: RMSNorm,
+// RoPE-pair rotation (+ the f16 KV-cache write), SwiGLU, argmax, and the
+// per-step bookkeeping kernel that feeds the next token on the device.
+#include "lkhip_common.h"
+
+// ---------------------------------------------------------------- RMSNorm
+// math::rmsnorm (src/math.rs:45-49): s = 1/sqrt(dot(x,x)/n + eps); y = (x*s)*w.
+// One block per row; fp32 sum of squares by wave reductions.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      uint32_t n, float eps, float* __restrict__ y) {
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* yr = y + (size_t)blockIdx.x * n;
+    __shared__ float part[4];
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = lk_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += 256) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+}
+
+hipError_t lk_rmsnorm_launch(const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* y,
+                             hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, w, n, eps, y);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------- RoPE
+// model::rope (src/model.rs:268-279): pair (i, i+hd/2) of each head turns by
+// pos * theta^(-2i/hd).  The inverse frequencies come from the host (same
+// powf as the CPU path), so (float)pos * f is bit-identical and only sinf /
+// cosf can differ.  Products are kept unfused, as the CPU computes them.
+__device__ __forceinline__ void rot_pair(float& a, float& b, float ang) {
+    const float s = sinf(ang), c = cosf(ang);
+    const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    const float nb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    a = na;
+    b = nb;
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, uint32_t rows, uint32_t n, uint32_t hd,
+                                                   const uint32_t* __restrict__ pos, const LkFreq fr) {
+    const uint32_t half = hd / 2;
+    const uint32_t pairs_per_row = n / 2;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (size_t)rows * pairs_per_row) return;
+    const uint32_t r = (uint32_t)(t / pairs_per_row), pr = (uint32_t)(t % pairs_per_row);
+    const uint32_t head = pr / half, i = pr % half;
+    float* hx = x + (size_t)r * n + (size_t)head * hd;
+    float a = hx[i], b = hx[i + half];
+    rot_pair(a, b, __fmul_rn((float)pos[r], fr.f[i]));
+    hx[i] = a;
+    hx[i + half] = b;
+}
+
+hipError_t lk_rope_launch(float* x, uint32_t rows, uint32_t n, uint32_t head_dim, const uint32_t* pos,
+                          const LkFreq& freq, hipStream_t st) {
+    const size_t total = (size_t)rows * (n / 2);
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, rows, n, head_dim,
+                       pos, freq);
+    return hipGetLastError();
+}
+
+// Decode step: rotate q in place and k, then write k and v of this position
+// into the f16 cache laid out [slot][kv_head][max_seq][64] (the KV append of
+// src/model.rs:228-231, stored f16 as the GPU path does).  qkv rows are
+// [q (n_heads*64) | k (n_kv*64) | v (n_kv*64)].
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, uint32_t n_heads, uint32_t n_kv,
+                                                      const LkFreq fr, const LkStepState* __restrict__ st,
+                                                      const uint32_t* __restrict__ pos_rows,
+                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                      uint32_t max_seq, uint64_t slot_stride,
+                                                      const uint32_t* __restrict__ slots) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t pos = pos_rows ? pos_rows[r] : st->pos;
+    const uint32_t slot = slots ? slots[r] : r;
+    const uint32_t qd = n_heads * 64, kvd = n_kv * 64;
+    float* row = qkv + (size_t)r * (qd + 2 * kvd);
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t nq_pairs = n_heads * 32, nk_pairs = n_kv * 32;
+    const float fpos = (float)pos;
+    if (t < nq_pairs) {
+        const uint32_t head = t / 32, i = t % 32;
+        float* h = row + head * 64;
+        float a = h[i], b = h[i + 32];
+        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        h[i] = a;
+        h[i + 32] = b;
+    } else if (t < nq_pairs + nk_pairs) {
+        const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
+        float* h = row + qd + head * 64;
+        float a = h[i], b = h[i + 32];
+        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        h[i] = a;
+        h[i + 32] = b;
+        uint16_t* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
+        dst[i] = __half_as_ushort(__float2half_rn(a));
+        dst[i + 32] = __half_as_ushort(__float2half_rn(b));
+    } else if (t < nq_pairs + nk_pairs + kvd) {
+        const uint32_t u = t - nq_pairs - nk_pairs, head = u / 64, d = u % 64;
+        const float v = row[qd + kvd + u];
+        vc[(size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d] = __half_as_ushort(__float2half_rn(v));
+    }
+}
+
+hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
+                             const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows, uint16_t* kcache,
+                             uint16_t* vcache, uint32_t max_seq, uint64_t slot_stride, const uint32_t* slots,
+                             hipStream_t st) {
+    const uint32_t work = n_heads * 32 + n_kv * 32 + n_kv * 64;
+    dim3 grid((work + 255) / 256, n_rows);
+    hipLaunchKernelGGL(rope_kv_kernel, grid, dim3(256), 0, st, qkv, n_heads, n_kv, freq, st_dev, pos_rows, kcache,
+                       vcache, max_seq, slot_stride, slots);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- SwiGLU
+// src/model.rs:247-249 with math::silu (src/math.rs:68-70): silu(g) * u,
+// silu(x) = x / (1 + exp(-x)).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     uint32_t n, float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float x = g[i];
+    out[i] = __fmul_rn(x / (1.0f + expf(-x)), u[i]);
+}
+
+hipError_t lk_swiglu_launch(const float* g, const float* u, uint32_t n, float* out, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, st, g, u, n, out);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- argmax
+__device__ __forceinline__ uint64_t max_key_block(uint64_t k) {
+    __shared__ uint64_t part[16];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = (blockDim.x + 63) / 64;
+        for (int w = 1; w < nw; w++) k = part[w] > k ? part[w] : k;
+        part[0] = k;
+    }
+    __syncthreads();
+    return part[0];
+}
+
+// sampler::argmax (src/sampler.rs:67-75) per row, first max wins.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ x, uint32_t n,
+                                                           uint32_t* __restrict__ out) {
+    const float* xr = x + (size_t)blockIdx.x * n;
+    uint64_t k = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t kk = lk_argmax_key(xr[i], i);
+        k = kk > k ? kk : k;
+    }
+    k = max_key_block(k);
+    if (threadIdx.x == 0) out[blockIdx.x] = lk_argmax_idx(k);
+}
+
+hipError_t lk_argmax_rows_launch(const float* x, uint32_t rows, uint32_t n, uint32_t* out, hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, st, x, n, out);
+    return hipGetLastError();
+}
+
+// End of a decode step: fold the lm_head's per-block argmax keys, then either
+// feed the next prompt id (prefill) or the argmax (greedy decode, as
+// generate.rs:101-118 does at -t 0), and advance the position.
+__global__ __launch_bounds__(1024) void step_finish_kernel(const uint64_t* __restrict__ keys, uint32_t n_keys,
+                                                           LkStepState* __restrict__ st,
+                                                           const uint32_t* __restrict__ feed,
+                                                           uint32_t* __restrict__ ids_out) {
+    uint64_t k = 0;
+    for (uint32_t i = threadIdx.x; i < n_keys; i += blockDim.x) k = keys[i] > k ? keys[i] : k;
+    k = max_key_block(k);
+    if (threadIdx.x == 0) {
+        const uint32_t best = lk_argmax_idx(k);
+        LkStepState s = *st;
+        if (s.n_feed > 0) {
+            s.token = feed[s.fed];
+            s.fed += 1;
+            s.n_feed -= 1;
+        } else {
+            if (ids_out) ids_out[s.n_out] = best;
+            s.n_out += 1;
+            s.token = best;
+        }
+        s.pos += 1;
+        *st = s;
+    }
+}
+
+hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepState* st_dev, const uint32_t* feed_ids,
+                                 uint32_t* ids_out, hipStream_t st) {
+    hipLaunchKernelGGL(step_finish_kernel, dim3(1), dim3(1024), 0, st, keys, n_keys, st_dev, feed_ids, ids_out);
+    return hipGetLastError();
+}

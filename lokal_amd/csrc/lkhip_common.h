@@ -1,0 +1,133 @@
+// lkhip_common.h -- shared device helpers and launch declarations for the
+// gfx950 decode kernels.  Wave size is 64 everywhere (CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define LK_WAVE 64
+
+// Weight types as stored on the device (GGUF ids; values unchanged, layout repacked).
+enum LkType : uint32_t { LK_F32 = 0, LK_F16 = 1, LK_Q8_0 = 8, LK_Q4_K = 12 };
+
+// f16 bits -> f32, exact (IEEE conversion; what half::f16::to_f32 computes,
+// src/gguf/dequant.rs:135-137).
+__device__ __forceinline__ float lk_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+__device__ __forceinline__ float lk_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, LK_WAVE);
+    return v;
+}
+__device__ __forceinline__ float lk_wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, LK_WAVE));
+    return v;
+}
+
+// A float made order-preserving as an unsigned key; the argmax key packs it
+// above the inverted index so that max(key) = (largest value, smallest index),
+// which is the "first max wins" rule of src/sampler.rs:67-75.
+__device__ __forceinline__ uint64_t lk_argmax_key(float v, uint32_t idx) {
+    uint32_t b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ uint32_t lk_argmax_idx(uint64_t key) { return 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu); }
+
+// A device weight matrix, repacked at upload (values unchanged):
+//   F16  : data = half  [rows][cols]
+//   Q8_0 : data = int8  [rows][cols]          aux = half [rows][cols/32]  (block scales d)
+//   Q4_K : data = uint8 [rows][cols/256][128] aux = uint8 [rows][cols/256][16]
+//          (aux = the super-block head: d, dmin f16 + 12 packed 6-bit scale/min bytes)
+struct LkDevW {
+    uint32_t type;
+    uint32_t rows, cols;
+    const uint8_t* data;
+    const uint8_t* aux;
+};
+
+// One output segment of a fused matvec launch (Q, K and V share one launch;
+// gate and up share one launch).
+struct LkSeg {
+    LkDevW w;
+    const float* bias;
+    float* out;
+};
+
+enum LkMvMode : int {
+    LK_MV_STORE = 0,   // out = W x (+ b)
+    LK_MV_ACC = 1,     // out += W x (+ b)       (residual add)
+    LK_MV_SWIGLU = 2,  // out = silu(W0 x) * (W1 x)  with seg[0] = gate, seg[1] = up
+    LK_MV_ARGMAX = 3   // out = W x, and per-block (max, first index) key into keys[blockIdx]
+};
+
+struct LkMvArgs {
+    LkSeg seg[3];
+    uint32_t nseg;
+    uint32_t total_rows;   // rows over all segments (SWIGLU: rows of one)
+    uint32_t cols;
+    const float* x;
+    uint64_t* keys;        // ARGMAX partial keys, one per block
+};
+
+// Host-side launchers (matvec.hip).
+struct LkMvPlan {
+    int rows_per_wave;
+    int nch;
+    unsigned blocks;
+};
+LkMvPlan lk_matvec_plan(uint32_t type, uint32_t total_rows, uint32_t cols, int mode);
+hipError_t lk_matvec_launch(const LkMvArgs& a, int mode, hipStream_t st, LkMvPlan* plan_out = nullptr);
+hipError_t lk_dequant_launch(const LkDevW& w, uint32_t row0, uint32_t nrows, float* out, hipStream_t st);
+hipError_t lk_gather_launch(const LkDevW& table, const uint32_t* ids, uint32_t n_ids, float* out, hipStream_t st);
+
+// Layer kernels (layer.hip).
+hipError_t lk_rmsnorm_launch(const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* y,
+                             hipStream_t st);
+// RoPE inverse frequencies theta^(-2i/hd), computed on the host with the
+// same powf the CPU path calls (src/model.rs:273) and passed by value.
+struct LkFreq {
+    float f[64];
+};
+hipError_t lk_rope_launch(float* x, uint32_t rows, uint32_t n, uint32_t head_dim, const uint32_t* pos,
+                          const LkFreq& freq, hipStream_t st);
+hipError_t lk_swiglu_launch(const float* g, const float* u, uint32_t n, float* out, hipStream_t st);
+hipError_t lk_argmax_rows_launch(const float* x, uint32_t rows, uint32_t n, uint32_t* out, hipStream_t st);
+
+// Decode-step glue kernels (layer.hip).
+struct LkStepState {
+    uint32_t token;   // token fed at this step
+    uint32_t pos;     // position of this step
+    uint32_t n_out;   // argmax ids written so far
+    uint32_t n_feed;  // prompt ids still to feed before argmax takes over
+    uint32_t fed;     // prompt ids fed so far
+    uint32_t pad[3];
+};
+hipError_t lk_embed_step_launch(const LkDevW& table, const LkStepState* st_dev, float* x, hipStream_t st);
+hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
+                             const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows,
+                             uint16_t* kcache, uint16_t* vcache, uint32_t max_seq, uint64_t slot_stride,
+                             const uint32_t* slots, hipStream_t st);
+hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepState* st_dev,
+                                 const uint32_t* feed_ids, uint32_t* ids_out, hipStream_t st);
+
+// Attention (attention.hip).  q rows of n_heads*64, caches f16
+// [seq][n_kv][max_seq][64]; ctx from ctx_len[seq] or, when null, st_dev->pos+1.
+struct LkAttnArgs {
+    const float* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    float* out;
+    float* part;            // scratch: [seq][n_heads][max_chunks][2 + 64]
+    const uint32_t* ctx_len;
+    const LkStepState* st;  // decode step state (single sequence, graph mode)
+    const uint32_t* slots;  // optional row -> cache slot map
+    uint32_t n_seq, n_heads, n_kv, max_seq;
+    uint64_t seq_stride;    // elements between two slots of the cache
+    uint64_t q_stride;      // floats between two sequences' q (and out) rows
+};
+uint32_t lk_attn_chunk(uint32_t max_seq);
+size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);
+hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st);

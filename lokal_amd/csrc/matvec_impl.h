@@ -1,0 +1,338 @@
+// matvec_impl.h -- the dequant-fused matvec kernel, one template for every
+// weight type.  Included by matvec_{q8_0,f16,q4_k}.hip, each of which
+// instantiates it for one type so the three compile in parallel.
+//
+// Work split: one wave (64 lanes) owns R output rows.  A row's payload is cut
+// into 16-byte "chunks" (Q8_0: 16 weights, F16: 8, Q4_K: 32 nibbles); lane l
+// owns chunks l, l+64, l+128, ...  Every 16-byte chunk is one global_load_dwordx4,
+// so a wave load is one contiguous 1 KiB run of the row.  A pass issues all
+// R x NCH chunk loads of a lane before any arithmetic, so each lane keeps
+// R*NCH*16 bytes in flight; NCH = ceil(chunks/64) covers a row in one pass for
+// every shape of the shipped configs.  x (f32) is read from L1/L2 and reused
+// across the R rows.  The per-lane f32 partials are reduced across the wave
+// by xor-shuffles (DPP/ds_swizzle), then lane 0 runs the epilogue
+// (bias, residual add, SwiGLU, or argmax key).
+#pragma once
+#include "lkhip_common.h"
+
+namespace lk {
+
+template <int WT> struct ChunkTraits;
+template <> struct ChunkTraits<LK_Q8_0> { static constexpr uint32_t elems = 16; };
+template <> struct ChunkTraits<LK_F16> { static constexpr uint32_t elems = 8; };
+template <> struct ChunkTraits<LK_Q4_K> { static constexpr uint32_t elems = 32; };
+
+typedef unsigned int lk_u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load of weight bytes (read once per token: nontemporal).
+__device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
+    const lk_u32x4 v = __builtin_nontemporal_load((const lk_u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float sbyte(uint32_t d, int k) {
+    return (float)((int32_t)(d << (24 - 8 * k)) >> 24);
+}
+
+// Q8_0: sum_j (i8)q_j * x_j over 16 weights; the block scale d is applied by
+// the caller (the CPU value (i8)q*d is exact, so a one-hot x returns it bit-for-bit).
+__device__ __forceinline__ float dot_q8(uint4 q, const float* __restrict__ x) {
+    const float4 x0 = *(const float4*)(x + 0), x1 = *(const float4*)(x + 4);
+    const float4 x2 = *(const float4*)(x + 8), x3 = *(const float4*)(x + 12);
+    float s0 = sbyte(q.x, 0) * x0.x, s1 = sbyte(q.x, 1) * x0.y;
+    s0 = fmaf(sbyte(q.x, 2), x0.z, s0); s1 = fmaf(sbyte(q.x, 3), x0.w, s1);
+    s0 = fmaf(sbyte(q.y, 0), x1.x, s0); s1 = fmaf(sbyte(q.y, 1), x1.y, s1);
+    s0 = fmaf(sbyte(q.y, 2), x1.z, s0); s1 = fmaf(sbyte(q.y, 3), x1.w, s1);
+    s0 = fmaf(sbyte(q.z, 0), x2.x, s0); s1 = fmaf(sbyte(q.z, 1), x2.y, s1);
+    s0 = fmaf(sbyte(q.z, 2), x2.z, s0); s1 = fmaf(sbyte(q.z, 3), x2.w, s1);
+    s0 = fmaf(sbyte(q.w, 0), x3.x, s0); s1 = fmaf(sbyte(q.w, 1), x3.y, s1);
+    s0 = fmaf(sbyte(q.w, 2), x3.z, s0); s1 = fmaf(sbyte(q.w, 3), x3.w, s1);
+    return s0 + s1;
+}
+
+__device__ __forceinline__ float2 h2x2(uint32_t v) {
+    return make_float2(__half2float(__ushort_as_half((uint16_t)(v & 0xFFFF))),
+                       __half2float(__ushort_as_half((uint16_t)(v >> 16))));
+}
+
+// F16: 8 weights.
+__device__ __forceinline__ float dot_f16(uint4 q, const float* __restrict__ x) {
+    const float4 x0 = *(const float4*)(x + 0), x1 = *(const float4*)(x + 4);
+    float2 a = h2x2(q.x), b = h2x2(q.y), c = h2x2(q.z), d = h2x2(q.w);
+    float s0 = a.x * x0.x, s1 = a.y * x0.y;
+    s0 = fmaf(b.x, x0.z, s0); s1 = fmaf(b.y, x0.w, s1);
+    s0 = fmaf(c.x, x1.x, s0); s1 = fmaf(c.y, x1.y, s1);
+    s0 = fmaf(d.x, x1.z, s0); s1 = fmaf(d.y, x1.w, s1);
+    return s0 + s1;
+}
+
+// scale_min_k4 (src/gguf/dequant.rs:141-150) on the 12 packed bytes held in
+// three dwords; j is lane-varying, so bytes are picked by shifts.
+__device__ __forceinline__ uint32_t kbyte(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t i) {
+    uint32_t w = (i < 4) ? s0 : ((i < 8) ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
+                                             uint32_t& m) {
+    if (j < 4) {
+        sc = kbyte(s0, s1, s2, j) & 63u;
+        m = kbyte(s0, s1, s2, j + 4) & 63u;
+    } else {
+        sc = (kbyte(s0, s1, s2, j + 4) & 0x0Fu) | ((kbyte(s0, s1, s2, j - 4) >> 6) << 4);
+        m = (kbyte(s0, s1, s2, j + 4) >> 4) | ((kbyte(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+// Q4_K: 16 bytes = 16 low nibbles (elements e0..e0+15 of sub-block 2g) and 16
+// high nibbles (e0+32.. of sub-block 2g+1).  Returns
+//   (d1*sum(q_lo x) - m1*sum(x_lo)) + (d2*sum(q_hi x) - m2*sum(x_hi))
+// with d1 = d*sc, m1 = dmin*m rounded first and the products kept unfused,
+// so a one-hot x yields d1*q - m1 exactly as dequant_row_ref does
+// (src/gguf/dequant.rs:462-483).
+__device__ __forceinline__ float dot_q4k(uint4 q, uint4 hdr, uint32_t k, const float* __restrict__ xlo) {
+    const float* xhi = xlo + 32;
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float sql = 0.f, sxl = 0.f, sqh = 0.f, sxh = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xl = *(const float4*)(xlo + 4 * i);
+        const float4 xh = *(const float4*)(xhi + 4 * i);
+        uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+        sql = fmaf((float)(lo & 0xFF), xl.x, sql);
+        sql = fmaf((float)((lo >> 8) & 0xFF), xl.y, sql);
+        sql = fmaf((float)((lo >> 16) & 0xFF), xl.z, sql);
+        sql = fmaf((float)(lo >> 24), xl.w, sql);
+        sqh = fmaf((float)(hi & 0xFF), xh.x, sqh);
+        sqh = fmaf((float)((hi >> 8) & 0xFF), xh.y, sqh);
+        sqh = fmaf((float)((hi >> 16) & 0xFF), xh.z, sqh);
+        sqh = fmaf((float)(hi >> 24), xh.w, sqh);
+        sxl += (xl.x + xl.y) + (xl.z + xl.w);
+        sxh += (xh.x + xh.y) + (xh.z + xh.w);
+    }
+    const float d = __half2float(__ushort_as_half((uint16_t)(hdr.x & 0xFFFF)));
+    const float dmin = __half2float(__ushort_as_half((uint16_t)(hdr.x >> 16)));
+    const uint32_t g = k >> 1;
+    uint32_t sc, m;
+    scale_min_k4(2 * g, hdr.y, hdr.z, hdr.w, sc, m);
+    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
+    scale_min_k4(2 * g + 1, hdr.y, hdr.z, hdr.w, sc, m);
+    const float d2 = __fmul_rn(d, (float)sc), m2 = __fmul_rn(dmin, (float)m);
+    const float lo_part = __fsub_rn(__fmul_rn(d1, sql), __fmul_rn(m1, sxl));
+    const float hi_part = __fsub_rn(__fmul_rn(d2, sqh), __fmul_rn(m2, sxh));
+    return lo_part + hi_part;
+}
+
+template <int WT>
+__device__ __forceinline__ size_t row_data_bytes(uint32_t cols) {
+    if constexpr (WT == LK_Q8_0) return cols;
+    else if constexpr (WT == LK_F16) return (size_t)cols * 2;
+    else return (size_t)(cols / 256) * 128;
+}
+template <int WT>
+__device__ __forceinline__ size_t row_aux_bytes(uint32_t cols) {
+    if constexpr (WT == LK_Q8_0) return (size_t)(cols / 32) * 2;
+    else if constexpr (WT == LK_F16) return 0;
+    else return (size_t)(cols / 256) * 16;
+}
+
+template <int WT, int NCH, int R, int MODE>
+__global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
+    constexpr int NR = (MODE == LK_MV_SWIGLU) ? 2 * R : R;
+    constexpr uint32_t CE = ChunkTraits<WT>::elems;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t row_base = wave * R;
+    const uint32_t cols = a.cols;
+    const uint32_t nchunk = cols / CE;
+    const float* __restrict__ x = a.x;
+
+    const uint8_t* rp[NR];
+    const uint8_t* ap[NR];
+    bool rv[NR];
+    uint32_t rr[NR];
+    int rs[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+        uint32_t gr = row_base + (uint32_t)(j % R);
+        int si = 0;
+        uint32_t r = gr;
+        if constexpr (MODE == LK_MV_SWIGLU) {
+            si = j / R;
+        } else {
+            if (a.nseg > 1 && r >= a.seg[0].w.rows) {
+                r -= a.seg[0].w.rows;
+                si = 1;
+                if (a.nseg > 2 && r >= a.seg[1].w.rows) {
+                    r -= a.seg[1].w.rows;
+                    si = 2;
+                }
+            }
+        }
+        rv[j] = gr < a.total_rows;
+        if (!rv[j]) r = 0;
+        rr[j] = r;
+        rs[j] = si;
+        const LkDevW& w = a.seg[si].w;
+        rp[j] = w.data + (size_t)r * row_data_bytes<WT>(cols);
+        ap[j] = w.aux + (size_t)r * row_aux_bytes<WT>(cols);
+    }
+
+    float acc[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) acc[j] = 0.f;
+
+    for (uint32_t base = 0; base < nchunk; base += 64 * NCH) {
+        uint4 wq[NR][NCH];
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const uint32_t c = base + (uint32_t)lane + 64u * i;
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                if (c < nchunk && rv[j]) wq[j][i] = ld_stream16(rp[j] + 16u * c);
+                else wq[j][i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        if constexpr (WT == LK_Q8_0) {
+            float dsc[NR][NCH];
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+#pragma unroll
+                for (int j = 0; j < NR; j++)
+                    dsc[j][i] = (c < nchunk && rv[j]) ? lk_h2f(((const uint16_t*)ap[j])[c >> 1]) : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+                if (c < nchunk) {
+                    const float* xc = x + (size_t)c * 16;
+#pragma unroll
+                    for (int j = 0; j < NR; j++) acc[j] = fmaf(dsc[j][i], dot_q8(wq[j][i], xc), acc[j]);
+                }
+            }
+        } else if constexpr (WT == LK_F16) {
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+                if (c < nchunk) {
+                    const float* xc = x + (size_t)c * 8;
+#pragma unroll
+                    for (int j = 0; j < NR; j++) acc[j] += dot_f16(wq[j][i], xc);
+                }
+            }
+        } else {  // Q4_K
+            uint4 hd[NR][NCH];
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+#pragma unroll
+                for (int j = 0; j < NR; j++)
+                    hd[j][i] = (c < nchunk && rv[j]) ? *(const uint4*)(ap[j] + 16u * (c >> 3)) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+                if (c < nchunk) {
+                    const uint32_t sb = c >> 3, k = c & 7;
+                    const float* xc = x + (size_t)sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
+#pragma unroll
+                    for (int j = 0; j < NR; j++) acc[j] += dot_q4k(wq[j][i], hd[j][i], k, xc);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < NR; j++) acc[j] = lk_wave_sum(acc[j]);
+
+    if constexpr (MODE == LK_MV_SWIGLU) {
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < R; j++) {
+                if (rv[j]) {
+                    const float g = acc[j], u = acc[R + j];
+                    a.seg[0].out[rr[j]] = g / (1.0f + expf(-g)) * u;
+                }
+            }
+        }
+    } else if constexpr (MODE == LK_MV_ARGMAX) {
+        __shared__ uint64_t best[4];
+        uint64_t key = 0;
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < R; j++) {
+                if (rv[j]) {
+                    const float v = acc[j];
+                    a.seg[0].out[rr[j]] = v;
+                    const uint64_t kk = lk_argmax_key(v, rr[j]);
+                    key = kk > key ? kk : key;
+                }
+            }
+            best[threadIdx.x >> 6] = key;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t k = best[0];
+            for (int w = 1; w < 4; w++) k = best[w] > k ? best[w] : k;
+            a.keys[blockIdx.x] = k;
+        }
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                if (rv[j]) {
+                    const LkSeg& s = a.seg[rs[j]];
+                    float v = acc[j];
+                    if (s.bias) v += s.bias[rr[j]];
+                    if constexpr (MODE == LK_MV_ACC) s.out[rr[j]] += v;
+                    else s.out[rr[j]] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int WT, int NCH, int R, int MODE>
+hipError_t launch_one(const LkMvArgs& a, unsigned blocks, hipStream_t st) {
+    hipLaunchKernelGGL((matvec_kernel<WT, NCH, R, MODE>), dim3(blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int WT, int NCH>
+hipError_t launch_r(const LkMvArgs& a, int mode, int R, unsigned blocks, hipStream_t st) {
+    switch (mode) {
+    case LK_MV_STORE:
+        if (R == 1) return launch_one<WT, NCH, 1, LK_MV_STORE>(a, blocks, st);
+        if (R == 2) return launch_one<WT, NCH, 2, LK_MV_STORE>(a, blocks, st);
+        return launch_one<WT, NCH, 4, LK_MV_STORE>(a, blocks, st);
+    case LK_MV_ACC:
+        if (R == 1) return launch_one<WT, NCH, 1, LK_MV_ACC>(a, blocks, st);
+        if (R == 2) return launch_one<WT, NCH, 2, LK_MV_ACC>(a, blocks, st);
+        return launch_one<WT, NCH, 4, LK_MV_ACC>(a, blocks, st);
+    case LK_MV_SWIGLU:
+        if (R == 1) return launch_one<WT, NCH, 1, LK_MV_SWIGLU>(a, blocks, st);
+        return launch_one<WT, NCH, 2, LK_MV_SWIGLU>(a, blocks, st);
+    case LK_MV_ARGMAX:
+        return launch_one<WT, NCH, 4, LK_MV_ARGMAX>(a, blocks, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int WT>
+hipError_t launch_type(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st) {
+    switch (nch) {
+    case 1: return launch_r<WT, 1>(a, mode, R, blocks, st);
+    case 2: return launch_r<WT, 2>(a, mode, R, blocks, st);
+    case 3: return launch_r<WT, 3>(a, mode, R, blocks, st);
+    case 4: return launch_r<WT, 4>(a, mode, R, blocks, st);
+    case 5: return launch_r<WT, 5>(a, mode, R, blocks, st);
+    case 6: return launch_r<WT, 6>(a, mode, R, blocks, st);
+    default: return launch_r<WT, 8>(a, mode, R, blocks, st);
+    }
+}
+
+}  // namespace lk
+
+hipError_t lk_matvec_launch_q8_0(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);
+hipError_t lk_matvec_launch_f16(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);
+hipError_t lk_matvec_launch_q4_k(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);

@@ -1,0 +1,208 @@
+"""The "hip" backend behind lokal's Engine / Session / Batcher seam
+(src/engine.rs:13-71), over the C ABI of include/lokal_hip.h.
+
+    engine = Engine.from_tensors(cfg, tensors)     # engine::create / create_metal_quant
+    sess = engine.session(max_seq)                 # Engine::session
+    logits = sess.forward(token, pos)              # Session::forward
+    logits = sess.prefill(ids)                     # Session::prefill (token loop)
+    ids = sess.decode_greedy(token, pos, n)        # generate.rs greedy loop, on device
+    b = engine.batcher(n_slots, max_seq)           # Engine::batcher
+    b.decode_step([BatchRow(token, pos, slot)])    # Batcher::decode_step
+
+Errors surface as LokalHipError carrying the backend's one-line reason.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import Config, LokalHipError, Profile, Row, TensorDesc, check, lib
+from .config import ModelConfig
+
+
+def create(backend: str, cfg: ModelConfig, tensors, llama_permuted: bool = False) -> "Engine":
+    """engine::create by backend name (src/engine.rs:76-111); this build has one: "hip"."""
+    if backend != "hip":
+        raise LokalHipError(-1, f'unknown backend "{backend}" — available: hip')
+    return Engine.from_tensors(cfg, tensors, llama_permuted)
+
+
+def _cfg_struct(cfg: ModelConfig) -> Config:
+    return Config(cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers, cfg.num_attention_heads,
+                  cfg.num_key_value_heads, cfg.vocab_size, cfg.head_dim, cfg.max_position_embeddings,
+                  cfg.rms_norm_eps, cfg.rope_theta)
+
+
+def _f32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _u32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+@dataclass
+class BatchRow:
+    """One active request in a batched decode step (src/engine.rs:30-34)."""
+    token: int
+    pos: int
+    slot: int
+
+
+class Engine:
+    name = "hip"
+
+    def __init__(self, handle, cfg: ModelConfig):
+        self._h = handle
+        self.cfg = cfg
+
+    @classmethod
+    def from_tensors(cls, cfg: ModelConfig, tensors, llama_permuted: bool = False) -> "Engine":
+        L = lib()
+        arr = (TensorDesc * len(tensors))()
+        keep = []
+        for i, t in enumerate(tensors):
+            data = np.ascontiguousarray(t.data).view(np.uint8).reshape(-1)
+            keep.append(data)
+            name = t.name.encode()
+            keep.append(name)
+            dims = (C.c_uint64 * 2)(*(list(t.dims) + [0])[:2])
+            arr[i] = TensorDesc(name, t.ggml_type, len(t.dims), dims, data.ctypes.data, data.size)
+        h = C.c_void_p()
+        check(L.lkhip_engine_create_tensors(C.byref(_cfg_struct(cfg)), arr, len(tensors), int(llama_permuted),
+                                            C.byref(h)))
+        return cls(h, cfg)
+
+    @classmethod
+    def from_gguf(cls, path: str) -> "Engine":
+        h = C.c_void_p()
+        check(lib().lkhip_engine_create_gguf(str(path).encode(), C.byref(h)))
+        c = Config()
+        check(lib().lkhip_engine_config(h, C.byref(c)))
+        cfg = ModelConfig(c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
+                          c.num_key_value_heads, c.vocab_size, c.rms_norm_eps, c.rope_theta,
+                          c.max_position_embeddings, c.head_dim)
+        return cls(h, cfg)
+
+    def config(self) -> ModelConfig:
+        return self.cfg
+
+    @property
+    def matvec_bytes(self) -> float:
+        """Algorithmic weight bytes one decode token streams through the matvecs."""
+        return float(lib().lkhip_engine_matvec_bytes(self._h))
+
+    def session(self, max_seq: int) -> "Session":
+        h = C.c_void_p()
+        check(lib().lkhip_session_create(self._h, max_seq, C.byref(h)))
+        return Session(self, h, max_seq)
+
+    def batcher(self, n_slots: int, max_seq: int) -> "Batcher":
+        h = C.c_void_p()
+        check(lib().lkhip_batch_create(self._h, n_slots, max_seq, C.byref(h)))
+        return Batcher(self, h, n_slots)
+
+    def close(self):
+        if self._h:
+            lib().lkhip_engine_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+class Session:
+    def __init__(self, engine: Engine, handle, max_seq: int):
+        self.engine = engine
+        self._h = handle
+        self.max_seq = max_seq
+        self.vocab = engine.cfg.vocab_size
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.vocab, dtype=np.float32)
+        check(lib().lkhip_session_forward(self._h, int(token), int(pos), _f32p(out)))
+        return out
+
+    def prefill(self, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.vocab, dtype=np.float32)
+        check(lib().lkhip_session_prefill(self._h, _u32p(ids), ids.size, _f32p(out)))
+        return out
+
+    def forward_batch(self, ids, pos0: int) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty((ids.size, self.vocab), dtype=np.float32)
+        check(lib().lkhip_session_forward_batch(self._h, _u32p(ids), ids.size, pos0, _f32p(out)))
+        return out
+
+    def decode_greedy(self, token: int, pos: int, n_steps: int, want_logits: bool = False):
+        ids = np.empty(max(n_steps, 1), dtype=np.uint32)
+        logits = np.empty(self.vocab, dtype=np.float32) if want_logits else None
+        check(lib().lkhip_session_decode_greedy(self._h, int(token), int(pos), int(n_steps), _u32p(ids),
+                                                _f32p(logits) if want_logits else None))
+        ids = ids[:n_steps]
+        return (ids, logits) if want_logits else ids
+
+    def read_kv(self, layer: int, pos: int, which_v: bool) -> np.ndarray:
+        out = np.empty(self.engine.cfg.kv_dim(), dtype=np.float32)
+        check(lib().lkhip_session_read_kv(self._h, layer, pos, int(which_v), _f32p(out)))
+        return out
+
+    def set_profiling(self, on: bool) -> None:
+        check(lib().lkhip_session_set_profiling(self._h, int(on)))
+
+    def profile(self, reset: bool = False) -> dict:
+        p = Profile()
+        check(lib().lkhip_session_profile(self._h, C.byref(p), int(reset)))
+        return p.as_dict()
+
+    def close(self):
+        if self._h:
+            lib().lkhip_session_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+class Batcher:
+    def __init__(self, engine: Engine, handle, n_slots: int):
+        self.engine = engine
+        self._h = handle
+        self.n_slots = n_slots
+        self.vocab = engine.cfg.vocab_size
+
+    def prefill(self, slot: int, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.vocab, dtype=np.float32)
+        check(lib().lkhip_batch_prefill(self._h, slot, _u32p(ids), ids.size, _f32p(out)))
+        return out
+
+    def decode_step(self, rows) -> list:
+        arr = (Row * len(rows))(*[Row(r.token, r.slot, r.pos) for r in rows])
+        out = np.empty((len(rows), self.vocab), dtype=np.float32)
+        check(lib().lkhip_batch_decode_step(self._h, arr, len(rows), _f32p(out)))
+        return [out[i] for i in range(len(rows))]
+
+    def close(self):
+        if self._h:
+            lib().lkhip_batch_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+__all__ = ["Engine", "Session", "Batcher", "BatchRow", "create", "LokalHipError", "_lib"]

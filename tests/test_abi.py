@@ -1,0 +1,83 @@
+"""The C-ABI library loads and exports exactly what include/lokal_hip.h
+declares; host-side refusals work without a GPU."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from lokal_amd import _lib, synth
+from lokal_amd.config import CONFIGS, ModelConfig
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "lokal_hip.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(lkhip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared()
+    for must in ("lkhip_engine_create_tensors", "lkhip_session_forward", "lkhip_session_prefill",
+                 "lkhip_batch_decode_step", "lkhip_q8_0_matvec", "lkhip_q4_k_matvec", "lkhip_dequant_rows",
+                 "lkhip_rmsnorm", "lkhip_rope_pairs", "lkhip_swiglu", "lkhip_embed_gather", "lkhip_attn_decode"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    missing = [n for n in declared() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_bindings_cover_the_header():
+    assert sorted(_lib.SIGNATURES) == declared()
+
+
+def test_no_device_here_is_reported_not_crashed():
+    L = _lib.lib()
+    n = L.lkhip_device_count()
+    assert n >= 0
+    if n == 0:
+        from lokal_amd import Engine, LokalHipError
+        cfg = ModelConfig(256, 512, 1, 4, 2, 300, 1e-6)
+        with pytest.raises(LokalHipError, match="no HIP device"):
+            Engine.from_tensors(cfg, synth.synth_model(cfg, synth.Q8_0, 0))
+
+
+def test_unknown_backend_refused():
+    from lokal_amd import LokalHipError, create
+    with pytest.raises(LokalHipError, match='unknown backend "metal"'):
+        create("metal", CONFIGS["qwen2.5-0.5b"], [])
+
+
+def test_synthetic_tensors_are_reproducible_and_sized():
+    cfg = ModelConfig(256, 512, 2, 4, 2, 300, 1e-6)
+    a = synth.synth_model(cfg, synth.Q8_0, seed=5, qkv_bias=True)
+    b = synth.synth_model(cfg, synth.Q8_0, seed=5, qkv_bias=True)
+    c = synth.synth_model(cfg, synth.Q8_0, seed=6, qkv_bias=True)
+    assert [t.name for t in a] == [t.name for t in b]
+    assert all(np.array_equal(x.data, y.data) for x, y in zip(a, b))
+    assert not np.array_equal(a[2].data, c[2].data)
+    for t in a:
+        n = int(np.prod(t.dims))
+        rows = t.dims[0] if len(t.dims) == 2 else 1
+        assert t.nbytes == rows * synth.row_bytes(t.ggml_type, n // rows)
+    q = next(t for t in a if t.name.endswith("q_proj.weight")).data.reshape(-1, 34)
+    d = q[:, :2].copy().view(np.float16).astype(np.float32)
+    assert (d >= 0).all() and np.isfinite(d).all()
+    assert q[:, 2:].view(np.int8).min() >= -127
+    k = synth.synth_model(cfg, synth.Q4_K, seed=1)[2].data.reshape(-1, 144)
+    dd = k[:, :4].copy().view(np.float16).astype(np.float32)
+    assert (dd >= 2.0 ** -10).all() and (dd <= 2.0 ** -6).all()
+
+
+def test_headline_config_bytes_per_token():
+    """Algorithmic Q8_0 bytes of one Qwen2.5-0.5B decode token: 493,961,216 weights x 34/32."""
+    c = CONFIGS["qwen2.5-0.5b"]
+    h, I, L, V = c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.vocab_size
+    per_layer = h * c.q_dim() + 2 * h * c.kv_dim() + c.q_dim() * h + 3 * h * I
+    weights = L * per_layer + V * h
+    assert weights == 493_961_216
+    assert weights * 34 // 32 == 524_833_792
