@@ -129,6 +129,10 @@ double lkhip_engine_matvec_bytes(const lkhip_engine* e);
 
 /* Engine::session (src/engine.rs:17): KV cache (f16, on device) for max_seq positions. */
 int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_session** out);
+/* Same with the KV cache element type chosen: LKHIP_F16 (the GPU path's
+ * format, src/gpu/metal.rs:3234-3235; what lkhip_session_create uses) or
+ * LKHIP_F32 (the CPU path's format, src/model.rs:114-128). */
+int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t kv_type, lkhip_session** out);
 void lkhip_session_destroy(lkhip_session* s);
 /* Session::forward (src/engine.rs:51): one token at pos -> vocab logits (host). */
 int lkhip_session_forward(lkhip_session* s, uint32_t token, size_t pos, float* logits_out);

@@ -70,6 +70,7 @@ SIGNATURES = {
     "lkhip_engine_config": (C.c_int, [_P, C.POINTER(Config)]),
     "lkhip_engine_matvec_bytes": (C.c_double, [_P]),
     "lkhip_session_create": (C.c_int, [_P, C.c_size_t, C.POINTER(_P)]),
+    "lkhip_session_create_ex": (C.c_int, [_P, C.c_size_t, C.c_uint32, C.POINTER(_P)]),
     "lkhip_session_destroy": (None, [_P]),
     "lkhip_session_forward": (C.c_int, [_P, C.c_uint32, C.c_size_t, _F]),
     "lkhip_session_prefill": (C.c_int, [_P, _U32, C.c_size_t, _F]),

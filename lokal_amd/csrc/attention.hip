@@ -31,7 +31,24 @@ __device__ __forceinline__ uint32_t attn_ctx(const LkAttnArgs& a, uint32_t seq) 
     return c < a.max_seq ? c : a.max_seq;  // never read past the cache
 }
 
-template <int G>
+// 8 consecutive cache elements as f32: f16 cache (one 16-byte load) or f32
+// cache (two 16-byte loads).
+__device__ __forceinline__ void load8(const uint16_t* p, float* o) {
+    const uint4 v = *(const uint4*)p;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+        o[2 * h] = lk_h2f((uint16_t)(w[h] & 0xFFFF));
+        o[2 * h + 1] = lk_h2f((uint16_t)(w[h] >> 16));
+    }
+}
+__device__ __forceinline__ void load8(const float* p, float* o) {
+    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+template <int G, typename KV>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t ctx = attn_ctx(a, seq);
@@ -40,8 +57,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     const uint32_t slot = a.slots ? a.slots[seq] : seq;
     const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
-    const uint16_t* __restrict__ K = a.k + kv_base;
-    const uint16_t* __restrict__ V = a.v + kv_base;
+    const KV* __restrict__ K = (const KV*)a.k + kv_base;
+    const KV* __restrict__ V = (const KV*)a.v + kv_base;
 
     __shared__ float qs[G][LK_HD];
     __shared__ float ps[4][G][64];
@@ -73,21 +90,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) s[g] = 0.f;
         if (valid) {
-            const uint4* krow = (const uint4*)(K + (size_t)p * LK_HD);
+            const KV* krow = K + (size_t)p * LK_HD;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const uint4 kv = krow[i];
-                const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+                float k8[8];
+                load8(krow + 8 * i, k8);
 #pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    const float k0 = lk_h2f((uint16_t)(kw[h] & 0xFFFF));
-                    const float k1 = lk_h2f((uint16_t)(kw[h] >> 16));
-                    const int d = i * 8 + h * 2;
+                for (int e = 0; e < 8; e++) {
 #pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        s[g] = fmaf(k0, qs[g][d], s[g]);
-                        s[g] = fmaf(k1, qs[g][d + 1], s[g]);
-                    }
+                    for (int g = 0; g < G; g++) s[g] = fmaf(k8[e], qs[g][8 * i + e], s[g]);
                 }
             }
         }
@@ -109,14 +120,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
         for (int j = 0; j < 8; j++) {
             const uint32_t pj = p0 + (uint32_t)j * 8 + sub;
             if (pj < ctx) {
-                const uint4 vv = *(const uint4*)(V + (size_t)pj * LK_HD + dq);
-                const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
                 float vf[8];
-#pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    vf[2 * h] = lk_h2f((uint16_t)(vw[h] & 0xFFFF));
-                    vf[2 * h + 1] = lk_h2f((uint16_t)(vw[h] >> 16));
-                }
+                load8(V + (size_t)pj * LK_HD + dq, vf);
 #pragma unroll
                 for (int g = 0; g < G; g++) {
                     const float pw = ps[w][g][j * 8 + sub];
@@ -200,17 +205,23 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
     const uint32_t G = a.n_heads / a.n_kv;
     const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     dim3 grid(max_chunks, a.n_kv, a.n_seq);
+#define LK_ATTN_CASE(g)                                                                         \
+    case g:                                                                                     \
+        if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(256), 0, st, a);  \
+        break;
     switch (G) {
-    case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(attn_partial_kernel<3>, grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(attn_partial_kernel<4>, grid, dim3(256), 0, st, a); break;
-    case 5: hipLaunchKernelGGL(attn_partial_kernel<5>, grid, dim3(256), 0, st, a); break;
-    case 6: hipLaunchKernelGGL(attn_partial_kernel<6>, grid, dim3(256), 0, st, a); break;
-    case 7: hipLaunchKernelGGL(attn_partial_kernel<7>, grid, dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL(attn_partial_kernel<8>, grid, dim3(256), 0, st, a); break;
+        LK_ATTN_CASE(1)
+        LK_ATTN_CASE(2)
+        LK_ATTN_CASE(3)
+        LK_ATTN_CASE(4)
+        LK_ATTN_CASE(5)
+        LK_ATTN_CASE(6)
+        LK_ATTN_CASE(7)
+        LK_ATTN_CASE(8)
     default: return hipErrorInvalidValue;
     }
+#undef LK_ATTN_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.n_seq), dim3(64), 0, st, a);

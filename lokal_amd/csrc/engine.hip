@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -383,7 +384,8 @@ struct lkhip_session {
     lkhip_engine* e = nullptr;
     size_t max_seq = 0;
     hipStream_t stream = nullptr;
-    DevBuf kc, vc;  // [layer][n_kv][max_seq][64] f16
+    DevBuf kc, vc;  // [layer][n_kv][max_seq][64], f16 or f32 (kv_f32)
+    int kv_f32 = 0;
     DevBuf x, xn, qkv, att, inner, logits, part, keys, state, feed, ids_out;
     LkStepState* h_state = nullptr;  // pinned
     float* h_logits = nullptr;       // pinned
@@ -463,9 +465,11 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             a.total_rows = e->qd + 2 * e->kvd;
             STEP(lk_matvec_launch(a, LK_MV_STORE, st), C_MATVEC, ly.q->bytes + ly.k->bytes + ly.v->bytes);
         }
-        uint16_t* kc = s->kc.as<uint16_t>() + (size_t)L * kv_layer_elems(s);
-        uint16_t* vc = s->vc.as<uint16_t>() + (size_t)L * kv_layer_elems(s);
+        const size_t kv_el = s->kv_f32 ? 4 : 2;
+        uint8_t* kc = s->kc.as<uint8_t>() + (size_t)L * kv_layer_elems(s) * kv_el;
+        uint8_t* vc = s->vc.as<uint8_t>() + (size_t)L * kv_layer_elems(s) * kv_el;
         STEP(lk_rope_kv_launch(qkv, c.num_attention_heads, c.num_key_value_heads, e->freq, state, nullptr, 1, kc, vc,
+                               s->kv_f32,
                                (uint32_t)s->max_seq, 0, nullptr, st),
              C_OTHER, 0);
         {
@@ -473,6 +477,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             a.q = qkv;
             a.k = kc;
             a.v = vc;
+            a.kv_f32 = (uint32_t)s->kv_f32;
             a.out = s->att.as<float>();
             a.part = s->part.as<float>();
             a.st = state;
@@ -541,8 +546,14 @@ static int build_graph(lkhip_session* s) {
 }
 
 extern "C" int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_session** out) {
+    return lkhip_session_create_ex(e, max_seq, LKHIP_F16, out);
+}
+
+extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t kv_type, lkhip_session** out) {
     if (!e || !out) return fail(LKHIP_E_INVALID, "session: null argument");
     *out = nullptr;
+    if (kv_type != LKHIP_F16 && kv_type != LKHIP_F32)
+        return fail(LKHIP_E_UNSUPPORTED, "session: the KV cache is F16 or F32, not %s", type_name(kv_type));
     if (max_seq == 0 || max_seq > 0x7FFFFFFF) return fail(LKHIP_E_INVALID, "session: max_seq must be in 1..2^31");
     (void)hipSetDevice(e->device);
     auto s = std::make_unique<lkhip_session>();
@@ -551,7 +562,8 @@ extern "C" int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_sessi
     const lkhip_config& c = e->cfg;
     HIP_OR_FAIL(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     int rc;
-    const size_t kv = (size_t)c.num_hidden_layers * kv_layer_elems(s.get()) * 2;
+    s->kv_f32 = kv_type == LKHIP_F32;
+    const size_t kv = (size_t)c.num_hidden_layers * kv_layer_elems(s.get()) * (s->kv_f32 ? 4 : 2);
     if ((rc = dev_alloc(s->kc, kv)) || (rc = dev_alloc(s->vc, kv))) return rc;
     if ((rc = dev_alloc(s->x, c.hidden_size * 4)) || (rc = dev_alloc(s->xn, c.hidden_size * 4)) ||
         (rc = dev_alloc(s->qkv, (e->qd + 2 * e->kvd) * 4)) || (rc = dev_alloc(s->att, e->qd * 4)) ||
@@ -565,7 +577,11 @@ extern "C" int lkhip_session_create(lkhip_engine* e, size_t max_seq, lkhip_sessi
     if ((rc = dev_alloc(s->feed, max_seq * 4)) || (rc = dev_alloc(s->ids_out, max_seq * 4))) return rc;
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_state, sizeof(LkStepState), hipHostMallocDefault));
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
-    if ((rc = build_graph(s.get()))) return rc;
+    // LKHIP_GRAPH=0 launches the step eagerly instead of replaying a HIP graph
+    // (for tools that cannot follow graph launches).
+    const char* g = getenv("LKHIP_GRAPH");
+    if (!(g && g[0] == '0'))
+        if ((rc = build_graph(s.get()))) return rc;
     *out = s.release();
     return LKHIP_OK;
 }
@@ -587,7 +603,13 @@ static int set_state(lkhip_session* s, uint32_t token, size_t pos, uint32_t n_fe
 // Runs one step: graph replay, or eager with events when profiling.
 static int run_step(lkhip_session* s) {
     if (!s->profiling) {
-        HIP_OR_FAIL(hipGraphLaunch(s->exec, s->stream));
+        if (s->exec) {
+            HIP_OR_FAIL(hipGraphLaunch(s->exec, s->stream));
+        } else {
+            Rec rec(s);
+            hipError_t err = enqueue_step(s, rec);
+            if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
+        }
         return LKHIP_OK;
     }
     Rec rec(s);
@@ -695,12 +717,19 @@ extern "C" int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t po
     const lkhip_config& c = s->e->cfg;
     if (layer >= c.num_hidden_layers || pos >= s->max_seq) return fail(LKHIP_E_INVALID, "read_kv: out of range");
     HIP_OR_FAIL(hipStreamSynchronize(s->stream));
-    const uint16_t* base = (which_v ? s->vc : s->kc).as<uint16_t>() + (size_t)layer * kv_layer_elems(s);
-    std::vector<uint16_t> h(64);
+    const size_t el = s->kv_f32 ? 4 : 2;
+    const uint8_t* base = (which_v ? s->vc : s->kc).as<uint8_t>() + (size_t)layer * kv_layer_elems(s) * el;
+    std::vector<uint8_t> h(64 * el);
     for (uint32_t kh = 0; kh < c.num_key_value_heads; kh++) {
-        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->max_seq + pos) * 64, 128, hipMemcpyDeviceToHost));
+        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->max_seq + pos) * 64 * el, 64 * el,
+                              hipMemcpyDeviceToHost));
+        if (s->kv_f32) {
+            memcpy(&out[kh * 64], h.data(), 256);
+            continue;
+        }
         for (int d = 0; d < 64; d++) {
-            uint32_t hb = h[d], sign = (hb >> 15) << 31, ex = (hb >> 10) & 31, m = hb & 1023, bits;
+            const uint16_t hb16 = (uint16_t)(h[2 * d] | (h[2 * d + 1] << 8));
+            uint32_t hb = hb16, sign = (hb >> 15) << 31, ex = (hb >> 10) & 31, m = hb & 1023, bits;
             if (ex == 0) {
                 if (m == 0) bits = sign;
                 else {

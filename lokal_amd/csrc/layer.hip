@@ -69,10 +69,14 @@ hipError_t lk_rope_launch(float* x, uint32_t rows, uint32_t n, uint32_t head_dim
 // into the f16 cache laid out [slot][kv_head][max_seq][64] (the KV append of
 // src/model.rs:228-231, stored f16 as the GPU path does).  qkv rows are
 // [q (n_heads*64) | k (n_kv*64) | v (n_kv*64)].
+__device__ __forceinline__ void kv_store(uint16_t* p, float v) { *p = __half_as_ushort(__float2half_rn(v)); }
+__device__ __forceinline__ void kv_store(float* p, float v) { *p = v; }
+
+template <typename KV>
 __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, uint32_t n_heads, uint32_t n_kv,
                                                       const LkFreq fr, const LkStepState* __restrict__ st,
                                                       const uint32_t* __restrict__ pos_rows,
-                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                      KV* __restrict__ kc, KV* __restrict__ vc,
                                                       uint32_t max_seq, uint64_t slot_stride,
                                                       const uint32_t* __restrict__ slots) {
     const uint32_t r = blockIdx.y;
@@ -97,24 +101,28 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, u
         rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
         h[i] = a;
         h[i + 32] = b;
-        uint16_t* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
-        dst[i] = __half_as_ushort(__float2half_rn(a));
-        dst[i + 32] = __half_as_ushort(__float2half_rn(b));
+        KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
+        kv_store(dst + i, a);
+        kv_store(dst + i + 32, b);
     } else if (t < nq_pairs + nk_pairs + kvd) {
         const uint32_t u = t - nq_pairs - nk_pairs, head = u / 64, d = u % 64;
         const float v = row[qd + kvd + u];
-        vc[(size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d] = __half_as_ushort(__float2half_rn(v));
+        kv_store(vc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d, v);
     }
 }
 
 hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
-                             const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows, uint16_t* kcache,
-                             uint16_t* vcache, uint32_t max_seq, uint64_t slot_stride, const uint32_t* slots,
+                             const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows, void* kcache,
+                             void* vcache, int kv_f32, uint32_t max_seq, uint64_t slot_stride, const uint32_t* slots,
                              hipStream_t st) {
     const uint32_t work = n_heads * 32 + n_kv * 32 + n_kv * 64;
     dim3 grid((work + 255) / 256, n_rows);
-    hipLaunchKernelGGL(rope_kv_kernel, grid, dim3(256), 0, st, qkv, n_heads, n_kv, freq, st_dev, pos_rows, kcache,
-                       vcache, max_seq, slot_stride, slots);
+    if (kv_f32)
+        hipLaunchKernelGGL(rope_kv_kernel<float>, grid, dim3(256), 0, st, qkv, n_heads, n_kv, freq, st_dev, pos_rows,
+                           (float*)kcache, (float*)vcache, max_seq, slot_stride, slots);
+    else
+        hipLaunchKernelGGL(rope_kv_kernel<uint16_t>, grid, dim3(256), 0, st, qkv, n_heads, n_kv, freq, st_dev,
+                           pos_rows, (uint16_t*)kcache, (uint16_t*)vcache, max_seq, slot_stride, slots);
     return hipGetLastError();
 }
 

@@ -108,7 +108,7 @@ struct LkStepState {
 hipError_t lk_embed_step_launch(const LkDevW& table, const LkStepState* st_dev, float* x, hipStream_t st);
 hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
                              const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows,
-                             uint16_t* kcache, uint16_t* vcache, uint32_t max_seq, uint64_t slot_stride,
+                             void* kcache, void* vcache, int kv_f32, uint32_t max_seq, uint64_t slot_stride,
                              const uint32_t* slots, hipStream_t st);
 hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepState* st_dev,
                                  const uint32_t* feed_ids, uint32_t* ids_out, hipStream_t st);
@@ -117,8 +117,8 @@ hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepSt
 // [seq][n_kv][max_seq][64]; ctx from ctx_len[seq] or, when null, st_dev->pos+1.
 struct LkAttnArgs {
     const float* q;
-    const uint16_t* k;
-    const uint16_t* v;
+    const void* k;          // f16 (uint16 bits) or f32 elements, see kv_f32
+    const void* v;
     float* out;
     float* part;            // scratch: [seq][n_heads][max_chunks][2 + 64]
     const uint32_t* ctx_len;
@@ -127,6 +127,7 @@ struct LkAttnArgs {
     uint32_t n_seq, n_heads, n_kv, max_seq;
     uint64_t seq_stride;    // elements between two slots of the cache
     uint64_t q_stride;      // floats between two sequences' q (and out) rows
+    uint32_t kv_f32;        // 1: the cache holds f32, 0: f16
 };
 uint32_t lk_attn_chunk(uint32_t max_seq);
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);

@@ -95,9 +95,13 @@ class Engine:
         """Algorithmic weight bytes one decode token streams through the matvecs."""
         return float(lib().lkhip_engine_matvec_bytes(self._h))
 
-    def session(self, max_seq: int) -> "Session":
+    def session(self, max_seq: int, kv_dtype: str = "f16") -> "Session":
+        """kv_dtype "f16" (the GPU path's cache format) or "f32" (the CPU path's)."""
+        kv = {"f16": _lib.LKHIP_F16, "f32": _lib.LKHIP_F32}.get(kv_dtype)
+        if kv is None:
+            raise LokalHipError(-1, f"session: the KV cache is f16 or f32, not {kv_dtype}")
         h = C.c_void_p()
-        check(lib().lkhip_session_create(self._h, max_seq, C.byref(h)))
+        check(lib().lkhip_session_create_ex(self._h, max_seq, kv, C.byref(h)))
         return Session(self, h, max_seq)
 
     def batcher(self, n_slots: int, max_seq: int) -> "Batcher":

@@ -78,6 +78,9 @@ def lib():
         L.oracle_forward.argtypes = [C.c_void_p, C.c_uint32, C.c_size_t, F32P]
         L.oracle_session_hidden.argtypes = [C.c_void_p, F32P]
         L.oracle_session_kv.argtypes = [C.c_void_p, C.c_uint32, C.c_size_t, C.c_int, F32P]
+        L.oracle_session_set_kv_f16.argtypes = [C.c_void_p, C.c_int]
+        L.oracle_f32_to_f16.argtypes = [C.c_float]
+        L.oracle_f32_to_f16.restype = C.c_uint16
         _lib = L
     return _lib
 
@@ -88,6 +91,10 @@ def _f32(a) -> np.ndarray:
 
 def f16_to_f32(bits: int) -> float:
     return float(lib().oracle_f16_to_f32(bits))
+
+
+def f32_to_f16(x: float) -> int:
+    return int(lib().oracle_f32_to_f16(x))
 
 
 def blk_elems(t: int) -> int:
@@ -201,6 +208,7 @@ class Model:
                           cfg.num_key_value_heads, cfg.vocab_size, cfg.head_dim or 0, cfg.rms_norm_eps,
                           cfg.rope_theta)
         self.cfg = cfg
+        self._sessions = []
         self._m = L.oracle_model_new(C.byref(oc))
         for t in tensors:
             data = np.ascontiguousarray(np.frombuffer(t.data, dtype=np.uint8) if not isinstance(t.data, np.ndarray)
@@ -214,10 +222,18 @@ class Model:
         if rc != 0:
             raise ValueError(f"oracle: model incomplete (code {rc})")
 
-    def session(self, max_seq: int) -> "Session":
-        return Session(self, max_seq)
+    def session(self, max_seq: int, kv_f16: bool = False) -> "Session":
+        """kv_f16: test-only variant storing K/V through f16 (the GPU cache format)."""
+        s = Session(self, max_seq)
+        if kv_f16:
+            lib().oracle_session_set_kv_f16(s._s, 1)
+        self._sessions.append(s)
+        return s
 
     def close(self):
+        for s in self._sessions:
+            s.close()
+        self._sessions = []
         if self._m:
             lib().oracle_model_free(self._m)
             self._m = None

@@ -63,6 +63,29 @@ ORACLE_API float oracle_f16_to_f32(uint16_t h) {
     return f;
 }
 
+/* f32 -> f16 bits, round to nearest even (what half::f16::from_f32 and the
+ * GPU's v_cvt_f16_f32 compute), with subnormals, overflow to inf and NaN. */
+ORACLE_API uint16_t oracle_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds past 65504 */
+    if (ax < 0x38800000u) {                                    /* f16 subnormal or zero */
+        if (ax < 0x33000000u) return (uint16_t)sign;           /* below half the smallest subnormal */
+        uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126 - e; /* value = m * 2^(e-150); target unit 2^-24 */
+        uint32_t q = m >> shift, rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t e = (ax >> 23) - 112, m = ax & 0x7fffffu;
+    uint32_t q = (e << 10) | (m >> 13), rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;
+    return (uint16_t)(sign | q);
+}
+
 static float f16_at(const uint8_t* p) { return oracle_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
 
 /* ------------------------------------------------------------- dequant */
@@ -389,6 +412,8 @@ typedef struct oracle_model {
 typedef struct oracle_session {
     const oracle_model* m;
     size_t max_seq;
+    uint32_t n_layers; /* kept so the session can be freed after its model */
+    int kv_f16;        /* store K/V rounded through f16, as the GPU cache does */
     float** k; /* per layer [max_seq * kv_dim], model::KvCache src/model.rs:114-128 */
     float** v;
     float *x, *xn, *q, *kk, *vv, *att, *ao, *gate, *up, *inner, *down;
@@ -507,6 +532,7 @@ ORACLE_API oracle_session* oracle_session_new(const oracle_model* m, size_t max_
     const oracle_config* c = &m->cfg;
     s->m = m;
     s->max_seq = max_seq;
+    s->n_layers = c->n_layers;
     s->k = (float**)calloc(c->n_layers, sizeof(float*));
     s->v = (float**)calloc(c->n_layers, sizeof(float*));
     for (uint32_t i = 0; i < c->n_layers; i++) {
@@ -529,7 +555,7 @@ ORACLE_API oracle_session* oracle_session_new(const oracle_model* m, size_t max_
 
 ORACLE_API void oracle_session_free(oracle_session* s) {
     if (!s) return;
-    for (uint32_t i = 0; i < s->m->cfg.n_layers; i++) {
+    for (uint32_t i = 0; i < s->n_layers; i++) {
         free(s->k[i]);
         free(s->v[i]);
     }
@@ -561,6 +587,12 @@ ORACLE_API int oracle_forward(oracle_session* s, uint32_t token, size_t pos, flo
         lin_fwd(&b->v, s->xn, s->vv);
         oracle_rope(s->q, m->q_dim, pos, m->hd, c->rope_theta);
         oracle_rope(s->kk, m->kv_dim, pos, m->hd, c->rope_theta);
+        if (s->kv_f16) {
+            for (size_t i = 0; i < m->kv_dim; i++) {
+                s->kk[i] = oracle_f16_to_f32(oracle_f32_to_f16(s->kk[i]));
+                s->vv[i] = oracle_f16_to_f32(oracle_f32_to_f16(s->vv[i]));
+            }
+        }
         memcpy(s->k[layer] + pos * m->kv_dim, s->kk, m->kv_dim * 4);
         memcpy(s->v[layer] + pos * m->kv_dim, s->vv, m->kv_dim * 4);
         oracle_attention(s->q, s->k[layer], s->v[layer], pos, c->n_heads, c->n_kv_heads, m->hd, m->kv_dim, s->att);
@@ -577,6 +609,11 @@ ORACLE_API int oracle_forward(oracle_session* s, uint32_t token, size_t pos, flo
     lin_fwd(&m->lm_head, s->xn, logits);
     return 0;
 }
+
+/* Test-only variant: keep the KV cache in f16 precision (values rounded
+ * through f16 on store), the storage format of lokal's GPU path
+ * (src/gpu/metal.rs:3234-3235).  Off by default: the CPU path is f32. */
+ORACLE_API void oracle_session_set_kv_f16(oracle_session* s, int on) { s->kv_f16 = on; }
 
 /* The hidden state after the last block and before the final norm; lets a
  * test compare intermediate state. */

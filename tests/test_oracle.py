@@ -295,3 +295,14 @@ def test_oracle_refuses_out_of_range():
         s.forward(300, 0)
     with pytest.raises(ValueError):
         s.forward(1, 4)
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(12)
+    xs = np.concatenate([rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+                         np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e9, -1e9, 2.0 ** -24, 2.0 ** -25,
+                                   3 * 2.0 ** -26, 2.0 ** -14, np.inf, -np.inf], np.float32)]).astype(np.float32)
+    got = np.array([oracle.f32_to_f16(float(x)) for x in xs], np.uint16)
+    want = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert oracle.f32_to_f16(float("nan")) & 0x7c00 == 0x7c00
