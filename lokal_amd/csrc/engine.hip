@@ -16,6 +16,7 @@
 
 #include "../../include/lokal_hip.h"
 #include "lkhip_common.h"
+#include "fused.h"
 
 // ------------------------------------------------------------------ errors
 
@@ -219,6 +220,13 @@ struct lkhip_engine {
     LkFreq freq{};
     double matvec_bytes = 0;
     int device = 0;
+    // one-kernel decode step (fused.hip): per-layer descriptors on device and
+    // the instantiated shape it runs; fused_ok = 0 when no instantiation fits
+    DevBuf fused_layers;
+    int fused_ok = 0, fused_nchh = 0, fused_nchi = 0, fused_g = 0;
+    unsigned fused_blocks = 0;
+    size_t fused_lds = 0;
+    std::string fused_why;
 };
 
 struct Named {
@@ -274,6 +282,73 @@ static int upload_mat(std::unique_ptr<lkhip_weight>& w, const lkhip_tensor* t, s
         return fail(rc, "%s: %s", t->name, why.c_str());
     }
     w.reset(p);
+    return LKHIP_OK;
+}
+
+// Decides whether the one-kernel decode step (fused.hip) can run this model
+// and uploads its per-layer descriptors.  Models it cannot run keep the
+// per-stage kernels; LKHIP_FUSED=0 forces those.
+static int fused_setup(lkhip_engine* e) {
+    const lkhip_config& c = e->cfg;
+    e->fused_ok = 0;
+    const char* env = getenv("LKHIP_FUSED");
+    if (env && env[0] == '0') {
+        e->fused_why = "disabled by LKHIP_FUSED=0";
+        return LKHIP_OK;
+    }
+    const uint32_t wt = e->layers[0].q->dw.type;
+    for (const Layer& ly : e->layers)
+        for (auto* w : {ly.q.get(), ly.k.get(), ly.v.get(), ly.o.get(), ly.gate.get(), ly.up.get(), ly.down.get()})
+            if (w->dw.type != wt) {
+                e->fused_why = "mixed weight types";
+                return LKHIP_OK;
+            }
+    if (e->lm_head->dw.type != wt) {
+        e->fused_why = "lm_head type differs from the layer weights";
+        return LKHIP_OK;
+    }
+    const uint32_t ce = wt == LKHIP_Q8_0 ? 16 : wt == LKHIP_F16 ? 8 : 32;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size;
+    if (e->qd != h) {
+        e->fused_why = "q width differs from hidden size";
+        return LKHIP_OK;
+    }
+    e->fused_nchh = (int)((h / ce + 63) / 64);
+    e->fused_nchi = (int)((I / ce + 63) / 64);
+    e->fused_g = (int)(c.num_attention_heads / c.num_key_value_heads);
+    int cus = 0;
+    HIP_OR_FAIL(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
+    e->fused_blocks = (unsigned)cus;
+    const uint32_t nw = e->fused_blocks * (uint32_t)(lk_fused_threads() / 64);
+    if ((c.num_attention_heads + 2 * c.num_key_value_heads) * 32 > nw || h > nw) {
+        e->fused_why = "more rows per stage than waves";
+        return LKHIP_OK;
+    }
+    // LDS limit for the longest session the one-kernel step serves
+    e->fused_lds = lk_fused_lds_bytes(h, I, c.num_attention_heads, c.num_key_value_heads, (uint32_t)e->fused_g,
+                                      (LK_FUSED_MAX_SEQ + 63) / 64);
+    LkFusedArgs probe{};
+    hipError_t st = hipSuccess;
+    for (int kv32 = 0; kv32 < 2 && st == hipSuccess; kv32++)  // both KV cache types
+        st = lk_fused_launch(probe, wt, e->fused_nchh, e->fused_nchi, e->fused_g, kv32, e->fused_blocks, e->fused_lds,
+                             nullptr, true);
+    if (st != hipSuccess) {
+        (void)hipGetLastError();
+        e->fused_why = "no fused instantiation for this shape";
+        return LKHIP_OK;
+    }
+    std::vector<LkFusedLayer> hl(c.num_hidden_layers);
+    for (uint32_t L = 0; L < c.num_hidden_layers; L++) {
+        Layer& ly = e->layers[L];
+        hl[L] = LkFusedLayer{ly.q->dw, ly.k->dw, ly.v->dw, ly.o->dw, ly.gate->dw, ly.up->dw, ly.down->dw,
+                             ly.in_norm.as<float>(), ly.post_norm.as<float>(),
+                             ly.has_bias ? ly.bq.as<float>() : nullptr, ly.has_bias ? ly.bk.as<float>() : nullptr,
+                             ly.has_bias ? ly.bv.as<float>() : nullptr};
+    }
+    int rc = dev_alloc(e->fused_layers, hl.size() * sizeof(LkFusedLayer));
+    if (rc) return rc;
+    HIP_OR_FAIL(hipMemcpy(e->fused_layers.p, hl.data(), hl.size() * sizeof(LkFusedLayer), hipMemcpyHostToDevice));
+    e->fused_ok = 1;
     return LKHIP_OK;
 }
 
@@ -363,6 +438,7 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
     if (e->lm_head->dw.type == LKHIP_F32)
         return fail(LKHIP_E_UNSUPPORTED, "lm_head must be F16, Q8_0 or Q4_K on the hip backend");
     e->matvec_bytes += e->lm_head->bytes;
+    if ((rc = fused_setup(e.get()))) return rc;
     *out = e.release();
     return LKHIP_OK;
 }
@@ -392,6 +468,13 @@ struct lkhip_session {
     uint32_t n_keys = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // one-kernel decode step: exchange buffers, epoch counter, error flag
+    bool use_fused = false;
+    uint32_t max_chunks = 0;
+    size_t fused_lds = 0;
+    DevBuf xb, qb, pb, ab, xpb, ib, kb, epoch, err;
+    DevBuf trace;          // stage timestamps of one block (lkhip_session_set_trace)
+    int trace_block = -1;
     // profiling
     bool profiling = false;
     std::vector<hipEvent_t> ev;
@@ -451,6 +534,48 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         if ((err = (call)) != hipSuccess) return err; \
         if ((err = rec.mark(cat, bytes)) != hipSuccess) return err; \
     } while (0)
+
+    if (s->use_fused) {
+        LkFusedArgs a{};
+        a.layers = e->fused_layers.as<LkFusedLayer>();
+        a.n_layers = c.num_hidden_layers;
+        a.embed = e->embed->dw;
+        a.lm_head = e->lm_head->dw;
+        a.norm = e->norm.as<float>();
+        a.freq = e->freq;
+        a.h = h;
+        a.I = I;
+        a.nh = c.num_attention_heads;
+        a.nkv = c.num_key_value_heads;
+        a.vocab = c.vocab_size;
+        a.eps = c.rms_norm_eps;
+        a.kc = s->kc.p;
+        a.vc = s->vc.p;
+        a.kv_layer = kv_layer_elems(s);
+        a.max_seq = (uint32_t)s->max_seq;
+        a.max_chunks = s->max_chunks;
+        a.st = state;
+        a.epoch = s->epoch.as<uint32_t>();
+        a.err = s->err.as<uint32_t>();
+        a.feed = s->feed.as<uint32_t>();
+        a.ids_out = s->ids_out.as<uint32_t>();
+        a.logits = s->logits.as<float>();
+        a.xb = s->xb.as<uint64_t>();
+        a.qb = s->qb.as<uint64_t>();
+        a.pb = s->pb.as<uint64_t>();
+        a.ab = s->ab.as<uint64_t>();
+        a.xpb = s->xpb.as<uint64_t>();
+        a.ib = s->ib.as<uint64_t>();
+        a.kb = s->kb.as<uint64_t>();
+        a.trace = s->trace_block >= 0 ? s->trace.as<uint64_t>() : nullptr;
+        a.trace_block = (uint32_t)(s->trace_block >= 0 ? s->trace_block : 0);
+        // The one kernel streams every matvec weight of the step: its time is
+        // the dequant-matvec time of the token.
+        STEP(lk_fused_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, s->kv_f32,
+                             e->fused_blocks, s->fused_lds, st, false),
+             C_MATVEC, e->matvec_bytes);
+        return hipSuccess;
+    }
 
     STEP(lk_embed_step_launch(e->embed->dw, state, x, st), C_OTHER, 0);
     for (uint32_t L = 0; L < c.num_hidden_layers; L++) {
@@ -575,6 +700,22 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
     if ((rc = dev_alloc(s->keys, (size_t)s->n_keys * 8))) return rc;
     if ((rc = dev_alloc(s->state, sizeof(LkStepState)))) return rc;
     if ((rc = dev_alloc(s->feed, max_seq * 4)) || (rc = dev_alloc(s->ids_out, max_seq * 4))) return rc;
+    if (e->fused_ok && max_seq <= LK_FUSED_MAX_SEQ) {
+        const size_t h = c.hidden_size, I = c.intermediate_size, G = (size_t)e->fused_g;
+        const size_t qkvd = e->qd + 2 * e->kvd;
+        s->max_chunks = (uint32_t)((max_seq + 63) / 64);
+        if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
+            (rc = dev_alloc(s->pb, 2 * (size_t)c.num_key_value_heads * s->max_chunks * G * 66 * 8)) ||
+            (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
+            (rc = dev_alloc(s->ib, 2 * I * 8)) || (rc = dev_alloc(s->kb, (size_t)e->fused_blocks * 2 * 8)) ||
+            (rc = dev_alloc(s->epoch, 4)) || (rc = dev_alloc(s->err, 4)))
+            return rc;
+        const uint32_t one = 1;
+        HIP_OR_FAIL(hipMemcpy(s->epoch.p, &one, 4, hipMemcpyHostToDevice));
+        s->fused_lds = lk_fused_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads,
+                                          c.num_key_value_heads, (uint32_t)e->fused_g, s->max_chunks);
+        s->use_fused = true;
+    }
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_state, sizeof(LkStepState), hipHostMallocDefault));
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
     // LKHIP_GRAPH=0 launches the step eagerly instead of replaying a HIP graph
@@ -650,10 +791,37 @@ static int check_tok(lkhip_session* s, uint32_t token, size_t pos) {
     return LKHIP_OK;
 }
 
+// Waits for the session stream; if a bounded wait inside the one-kernel step
+// timed out, the session drops to the per-stage kernels and the call fails.
+static int sync_check(lkhip_session* s) {
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    if (!s->use_fused) return LKHIP_OK;
+    uint32_t flag = 0;
+    HIP_OR_FAIL(hipMemcpy(&flag, s->err.p, 4, hipMemcpyDeviceToHost));
+    if (!flag) return LKHIP_OK;
+    s->use_fused = false;
+    if (s->exec) {
+        (void)hipGraphExecDestroy(s->exec);
+        s->exec = nullptr;
+    }
+    if (s->graph) {
+        (void)hipGraphDestroy(s->graph);
+        s->graph = nullptr;
+    }
+    const char* g = getenv("LKHIP_GRAPH");
+    if (!(g && g[0] == '0')) {
+        int rc = build_graph(s);
+        if (rc) return rc;
+    }
+    return fail(LKHIP_E_HIP, "the one-kernel decode step timed out waiting on another workgroup (is every CU "
+                             "free?) — this session now runs the per-stage kernels; repeat the call");
+}
+
 static int copy_logits(lkhip_session* s, float* out) {
     const size_t n = s->e->cfg.vocab_size;
     HIP_OR_FAIL(hipMemcpyAsync(s->h_logits, s->logits.p, n * 4, hipMemcpyDeviceToHost, s->stream));
-    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    int rc = sync_check(s);
+    if (rc) return rc;
     memcpy(out, s->h_logits, n * 4);
     return LKHIP_OK;
 }
@@ -679,8 +847,7 @@ extern "C" int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size
     for (size_t i = 0; i < n; i++)
         if ((rc = run_step(s))) return rc;
     if (logits_out) return copy_logits(s, logits_out);
-    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
-    return LKHIP_OK;
+    return sync_check(s);
 }
 
 extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n, size_t pos0,
@@ -706,7 +873,7 @@ extern "C" int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, siz
     for (size_t i = 0; i < n_steps; i++)
         if ((rc = run_step(s))) return rc;
     HIP_OR_FAIL(hipMemcpyAsync(s->h_logits, s->ids_out.p, n_steps * 4, hipMemcpyDeviceToHost, s->stream));
-    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    if ((rc = sync_check(s))) return rc;
     memcpy(ids_out, s->h_logits, n_steps * 4);
     if (logits_last) return copy_logits(s, logits_last);
     return LKHIP_OK;
@@ -762,6 +929,43 @@ extern "C" int lkhip_session_profile(lkhip_session* s, lkhip_profile* out, int r
     if (!s || !out) return fail(LKHIP_E_INVALID, "null argument");
     *out = s->prof;
     if (reset) s->prof = lkhip_profile{};
+    return LKHIP_OK;
+}
+
+static int rebuild_graph(lkhip_session* s) {
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    if (s->exec) {
+        (void)hipGraphExecDestroy(s->exec);
+        s->exec = nullptr;
+    }
+    if (s->graph) {
+        (void)hipGraphDestroy(s->graph);
+        s->graph = nullptr;
+    }
+    const char* g = getenv("LKHIP_GRAPH");
+    if (g && g[0] == '0') return LKHIP_OK;
+    return build_graph(s);
+}
+
+extern "C" int lkhip_session_set_trace(lkhip_session* s, int block) {
+    if (!s) return fail(LKHIP_E_INVALID, "null session");
+    if (!s->use_fused) return fail(LKHIP_E_UNSUPPORTED, "stage tracing needs the one-kernel decode step");
+    if (block >= (int)s->e->fused_blocks) return fail(LKHIP_E_INVALID, "trace block %d out of range", block);
+    if (block >= 0 && !s->trace.p) {
+        int rc = dev_alloc(s->trace, lk_fused_trace_len(s->e->cfg.num_hidden_layers) * 8);
+        if (rc) return rc;
+    }
+    s->trace_block = block < 0 ? -1 : block;
+    return rebuild_graph(s);
+}
+
+extern "C" int lkhip_session_trace(lkhip_session* s, uint64_t* ticks, size_t n) {
+    if (!s || !ticks) return fail(LKHIP_E_INVALID, "null argument");
+    const size_t len = lk_fused_trace_len(s->e->cfg.num_hidden_layers);
+    if (s->trace_block < 0) return fail(LKHIP_E_INVALID, "stage tracing is off");
+    if (n < len) return fail(LKHIP_E_INVALID, "trace needs %zu entries", len);
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    HIP_OR_FAIL(hipMemcpy(ticks, s->trace.p, len * 8, hipMemcpyDeviceToHost));
     return LKHIP_OK;
 }
 

@@ -1,0 +1,60 @@
+// fused.h -- arguments of the persistent one-kernel decode step (fused.hip).
+#pragma once
+#include "lkhip_common.h"
+
+struct LkFusedLayer {
+    LkDevW q, k, v, o, gate, up, down;
+    const float* in_norm;
+    const float* post_norm;
+    const float* bq;  // null when the model has no q/k/v biases
+    const float* bk;
+    const float* bv;
+};
+
+struct LkFusedArgs {
+    const LkFusedLayer* layers;  // device array, n_layers entries
+    uint32_t n_layers;
+    LkDevW embed, lm_head;
+    const float* norm;
+    LkFreq freq;
+    uint32_t h, I, nh, nkv, vocab;
+    float eps;
+    // session state
+    void* kc;            // KV cache [layer][kv_head][max_seq][64], f16 or f32
+    void* vc;
+    uint64_t kv_layer;   // elements per layer of one cache
+    uint32_t max_seq, max_chunks;
+    LkStepState* st;
+    uint32_t* epoch;     // token counter of the exchange epochs
+    uint32_t* err;       // set when a bounded wait timed out
+    const uint32_t* feed;
+    uint32_t* ids_out;
+    float* logits;
+    // exchange buffers of (f32 | epoch) words, two copies by layer parity
+    uint64_t* xb;   // [2][h]        layer input x
+    uint64_t* qb;   // [2][qd+2kvd]  rotated q, this token's k and v
+    uint64_t* pb;   // [2][nkv][max_chunks][G][66] attention partials (m, l, acc[64])
+    uint64_t* ab;   // [2][qd]       attention output
+    uint64_t* xpb;  // [2][h]        x after the attention residual
+    uint64_t* ib;   // [2][I]        SwiGLU output
+    uint64_t* kb;   // [blocks][2]   argmax keys
+    // optional stage timestamps (s_memrealtime, 100 MHz) of one block:
+    // [0] start, [1] after the embedding, [2 + 6L + s] after stage s of layer
+    // L, then after the final norm, after lm_head, and (block 0) at the end
+    uint64_t* trace;
+    uint32_t trace_block;
+};
+// ... followed by 8 sub-steps of layer 1's attention stage (when the traced
+// block runs an attention unit there).
+inline size_t lk_fused_trace_len(uint32_t n_layers) { return 2 + 6 * (size_t)n_layers + 4 + 8; }
+
+// LDS of one workgroup for sessions of up to max_chunks 64-position tiles.
+size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks);
+// Longest session (positions) the one-kernel step serves; longer ones run the
+// per-stage kernels (their attention partials would not fit in LDS).
+#define LK_FUSED_MAX_SEQ 4096u
+int lk_fused_threads();
+// setup=true checks the shape is instantiated, sets the LDS limit and checks
+// one block fits per CU; setup=false launches `blocks` blocks.
+hipError_t lk_fused_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, int kv_f32, unsigned blocks,
+                           size_t lds, hipStream_t st, bool setup);

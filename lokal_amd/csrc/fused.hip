@@ -1,0 +1,812 @@
+// fused.hip -- the whole decode step of one token (Model::forward,
+// src/model.rs:196-262) as ONE persistent kernel on gfx950.
+//
+// Why: batch-1 decode is a chain of ~5 dependent stages per layer (QKV ->
+// attention -> o_proj -> gate/up -> down).  As separate kernels every stage
+// pays a kernel boundary (~1.6 us in a HIP graph on MI355X) plus a cold
+// weight fetch on the critical path.  Here one workgroup per CU runs every
+// stage; a stage
+//   1. issues the HBM loads of its own weight rows (they do not depend on
+//      the activations, so they are in flight while the wave waits),
+//   2. waits for its input vector, which the producing stage published as
+//      64-bit words (f32 value | 32-bit epoch) with agent-coherent stores --
+//      the wait and the data read are the same memory round trip, no
+//      atomics and no grid barrier,
+//   3. computes and publishes its outputs the same way.
+// The epoch is (token counter, layer), so buffers never need clearing;
+// consecutive layers alternate between two copies of each buffer.
+//
+// Stage map (matvec units are spread wave-major over all CUs):
+//   S1 QKV      RMSNorm(x) + q/k/v rows in (i, i+32) pairs + bias + RoPE;
+//               k/v rounded to the cache type, written to the KV cache and
+//               published for this token's attention
+//   S2 attn     one workgroup per (kv head, span of 8 x 64 positions):
+//               flash-decoding over the span, K/V of cached positions loaded
+//               before the wait for q; one (m, l, acc) partial per query head
+//   S4 o_proj   folds the span partials of every head in LDS, o_proj + residual -> x'
+//   S5 gate/up  RMSNorm(x') + SwiGLU  -> inner
+//   S6 down     + residual            -> x of the next layer
+//   final       RMSNorm + lm_head (+ logits, rows double-buffered) + argmax
+//               keys; block 0 folds them and advances the step state.
+// Weight rows of a stage are issued one stage early (o_proj with gate/up,
+// gate/up with down, down with the next layer's q/k/v).
+// Every wait is bounded: on timeout the kernel raises an error flag, stops
+// waiting everywhere, and the host reports the failure.
+#include "lkhip_common.h"
+#include "matvec_impl.h"
+#include "fused.h"
+
+#define FW 8
+#define FT (FW * 64)
+#define FCH 64
+// Stage timestamp of the traced block (thread 0 only).
+// Sub-steps of layer 1's attention unit (traced block, thread 0).
+#define LKF_SUB(k)                                                                    \
+    do {                                                                              \
+        if (L == 1 && a.trace && blockIdx.x == a.trace_block && threadIdx.x == 0)     \
+            a.trace[2 + 6 * nL + 4 + (k)] = __builtin_amdgcn_s_memrealtime();         \
+    } while (0)
+#define LKF_MARK(k)                                                          \
+    do {                                                                     \
+        if (a.trace && blockIdx.x == a.trace_block && threadIdx.x == 0)      \
+            a.trace[(k)] = __builtin_amdgcn_s_memrealtime();                 \
+    } while (0)
+
+namespace lkf {
+
+using namespace lk;
+
+struct Ctx {
+    const LkFusedArgs* a;
+    uint32_t* err;
+    int lane, wave, gw, nw;
+};
+
+__device__ __forceinline__ uint64_t word(float v, uint32_t ep) {
+    return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
+}
+__device__ __forceinline__ void publish(uint64_t* p, float v, uint32_t ep) {
+    __hip_atomic_store(p, word(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Spin until word p carries epoch ep; returns its value.  Bounded: after
+// ~2^21 polls (tens of ms) the error flag is raised and every later wait
+// returns at once, so the grid always drains.
+__device__ __forceinline__ float await(const Ctx& c, const uint64_t* p, uint32_t ep) {
+    uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)(w >> 32) == ep) return __uint_as_float((uint32_t)w);
+    for (uint32_t n = 0;; n++) {
+        __builtin_amdgcn_s_sleep(1);
+        w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(w >> 32) == ep) break;
+        if ((n & 255) == 255) {
+            if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+            if (n > (1u << 21)) {
+                __hip_atomic_store(c.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    return __uint_as_float((uint32_t)w);
+}
+
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Words src[i0 + k*step], k < 8, i < n, into dst[...]: all eight loads are in
+// flight together; only words not yet carrying the epoch are polled again.
+__device__ __forceinline__ void await8(const Ctx& c, const uint64_t* src, uint32_t i0, uint32_t step, uint32_t n,
+                                       uint32_t ep, float* dst) {
+    uint64_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t i = i0 + k * step;
+        w[k] = i < n ? ld_word(src + i) : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t i = i0 + k * step;
+        if (i < n) dst[i] = (uint32_t)(w[k] >> 32) == ep ? __uint_as_float((uint32_t)w[k]) : await(c, src + i, ep);
+    }
+}
+
+// Block-cooperative: wait for n published words into LDS.
+__device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst) {
+    __syncthreads();  // every wave is done reading dst from the previous stage
+    for (uint32_t i = threadIdx.x; i < n; i += 8 * FT) await8(c, src, i, FT, n, ep, dst);
+    __syncthreads();
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = lk_wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < FW; i++) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// math::rmsnorm (src/math.rs:45-49) of the LDS vector xr into xo.
+__device__ __forceinline__ void rmsnorm_lds(const float* xr, const float* __restrict__ g, uint32_t n, float eps,
+                                            float* xo, float* red) {
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += FT) ss = fmaf(xr[i], xr[i], ss);
+    const float tot = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += FT) xo[i] = __fmul_rn(__fmul_rn(xr[i], scale), g[i]);
+    __syncthreads();
+}
+
+// One weight row held in registers: its 16-byte chunks for this lane.
+template <int WT, int NCH>
+struct Row {
+    uint4 q[NCH];
+    uint4 hd[NCH];  // Q4_K super-block heads
+    uint32_t d[NCH];  // Q8_0 block scales, raw f16 bits: converted at use, so issuing never waits
+};
+
+template <int WT>
+__device__ __forceinline__ const uint8_t* row_ptr(const LkDevW& w, uint32_t r) {
+    return w.data + (size_t)r * row_data_bytes<WT>(w.cols);
+}
+template <int WT>
+__device__ __forceinline__ const uint8_t* aux_ptr(const LkDevW& w, uint32_t r) {
+    return w.aux + (size_t)r * row_aux_bytes<WT>(w.cols);
+}
+
+template <int WT, int NCH>
+__device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint32_t r, int lane) {
+    const uint32_t nchunk = w.cols / ChunkTraits<WT>::elems;
+    const uint8_t* rp = row_ptr<WT>(w, r);
+    const uint8_t* ap = aux_ptr<WT>(w, r);
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch = (uint32_t)lane + 64u * i;
+        const bool ok = ch < nchunk;
+        R.q[i] = ok ? ld_stream16(rp + 16u * ch) : make_uint4(0, 0, 0, 0);
+        if constexpr (WT == LK_Q8_0) R.d[i] = ok ? (uint32_t)((const uint16_t*)ap)[ch >> 1] : 0u;
+        if constexpr (WT == LK_Q4_K) R.hd[i] = ok ? *(const uint4*)(ap + 16u * (ch >> 3)) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+// This lane's partial dot of the row with x (LDS); reduce across the wave after.
+template <int WT, int NCH>
+__device__ __forceinline__ float row_dot(const Row<WT, NCH>& R, const float* x, uint32_t cols, int lane) {
+    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch = (uint32_t)lane + 64u * i;
+        if (ch < nchunk) {
+            if constexpr (WT == LK_Q8_0) {
+                acc = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], x + ch * 16), acc);
+            } else if constexpr (WT == LK_F16) {
+                acc += dot_f16(R.q[i], x + ch * 8);
+            } else {
+                const uint32_t sb = ch >> 3, k = ch & 7;
+                acc += dot_q4k(R.q[i], R.hd[i], k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
+            }
+        }
+    }
+    return acc;
+}
+
+// row_dot with this lane's x slice already in registers (xr[i] = the x values
+// chunk i of the lane multiplies; Q4_K: 16 low-nibble then 16 high-nibble values).
+template <int WT, int NCH>
+__device__ __forceinline__ float row_dot_reg(const Row<WT, NCH>& R, const float (&xr)[NCH][ChunkTraits<WT>::elems],
+                                             uint32_t cols, int lane) {
+    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch = (uint32_t)lane + 64u * i;
+        if (ch < nchunk) {
+            if constexpr (WT == LK_Q8_0) {
+                acc = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], xr[i]), acc);
+            } else if constexpr (WT == LK_F16) {
+                acc += dot_f16(R.q[i], xr[i]);
+            } else {
+                float xx[64];  // dot_q4k reads x[0..15] and x[32..47]
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    xx[e] = xr[i][e];
+                    xx[32 + e] = xr[i][16 + e];
+                }
+                acc += dot_q4k(R.q[i], R.hd[i], ch & 7, xx);
+            }
+        }
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float kv_round(float v, bool f32) {
+    return f32 ? v : __half2float(__float2half_rn(v));
+}
+__device__ __forceinline__ void kv_put(uint16_t* p, float v) { *p = __half_as_ushort(__float2half_rn(v)); }
+__device__ __forceinline__ void kv_put(float* p, float v) { *p = v; }
+__device__ __forceinline__ void kv8(const uint16_t* p, float* o) {
+    const uint4 v = *(const uint4*)p;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+        o[2 * h] = lk_h2f((uint16_t)(w[h] & 0xFFFF));
+        o[2 * h + 1] = lk_h2f((uint16_t)(w[h] >> 16));
+    }
+}
+__device__ __forceinline__ void kv8(const float* p, float* o) {
+    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+__device__ __forceinline__ void rot(float& x0, float& x1, float ang) {
+    const float s = sinf(ang), c = cosf(ang);
+    const float n0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+    const float n1 = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+    x0 = n0;
+    x1 = n1;
+}
+
+// Cache-chunk packing of values held as f32: 4 floats (f32 cache) or 8
+// f16-representable floats (f16 cache: exact) into one 16-byte chunk.
+__device__ __forceinline__ uint32_t h2bits(float a, float b) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+}
+__device__ __forceinline__ uint4 pack4(const float* v, bool f32) {
+    if (f32) return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+    return make_uint4(h2bits(v[0], v[1]), h2bits(v[2], v[3]), h2bits(v[4], v[5]), h2bits(v[6], v[7]));
+}
+// Elements 8q..8q+7 of a raw cache row as f32.
+template <int N>
+__device__ __forceinline__ void unpack8(const uint4 (&raw)[N], int q, bool f32, float* o) {
+    if (f32) {
+        const uint4 a0 = raw[2 * q], a1 = raw[(2 * q + 1) < N ? 2 * q + 1 : 0];
+        o[0] = __uint_as_float(a0.x); o[1] = __uint_as_float(a0.y);
+        o[2] = __uint_as_float(a0.z); o[3] = __uint_as_float(a0.w);
+        o[4] = __uint_as_float(a1.x); o[5] = __uint_as_float(a1.y);
+        o[6] = __uint_as_float(a1.z); o[7] = __uint_as_float(a1.w);
+    } else {
+        const uint4 a = raw[q];
+        const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            o[2 * e] = lk_h2f((uint16_t)(w4[e] & 0xFFFF));
+            o[2 * e + 1] = lk_h2f((uint16_t)(w4[e] >> 16));
+        }
+    }
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int WT, int NCHH, int NCHI, typename KV, int G>
+__global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) {
+    extern __shared__ float lds[];
+    const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
+    const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
+    const uint32_t vmax = (I > h ? I : h) > qd ? (I > h ? I : h) : qd;
+    const uint32_t nspan_max = (a.max_chunks + FW - 1) / FW;
+    constexpr uint32_t WVF = 3 * G * 64 + 2 * G;  // P [G][64], acc [2 halves][G][64], m [G], l [G]
+    float* xin = lds;                 // vmax: the (normalised) input vector of a stage
+    float* xres = xin + vmax;         // h: the residual stream of this layer
+    float* red = xres + h;            // 16: block reductions
+    float* qg = red + 16;             // G*64 + 128: the group's q rows, this token's k and v
+    float* wv = qg + G * 64 + 128;    // FW * WVF: per wave P tile, acc, m, l
+    float* pbuf = wv + FW * WVF;      // nkv * nspan_max * G * 66: attention partials
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* wP = wv + wave * WVF;      // [G][64]
+    float* wA = wP + G * 64;          // [G][64]
+    float* wM = wA + 2 * G * 64;      // [G]
+    float* wL = wM + G;               // [G]
+    float* kcur = qg + G * 64;
+    float* vcur = kcur + 64;
+
+    Ctx c{&a, a.err, lane, wave, (int)(wave * gridDim.x + blockIdx.x), (int)(FW * gridDim.x)};
+    constexpr bool KV32 = sizeof(KV) == 4;
+    constexpr int KC = KV32 ? 16 : 8;  // 16-byte chunks in a 64-element cache row
+    const uint32_t base = a.epoch[0];
+    const LkStepState st = *a.st;
+    const uint32_t pos = st.pos, token = st.token;
+    const uint32_t nL = a.n_layers;
+    const float fpos = (float)pos;
+    const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
+    const uint32_t nspan = (ntile + FW - 1) / FW;   // one attention unit = FW tiles of one kv head
+
+    // S1 work of this wave: q/k/v rows (i, i+32) of one head
+    const uint32_t U1 = (nh + 2 * nkv) * 32;
+    const bool has1 = c.gw < (int)U1;
+    uint32_t kind = 0, head = 0, ip = 0;
+    if (has1) {
+        const uint32_t hh = (uint32_t)c.gw / 32;
+        ip = (uint32_t)c.gw % 32;
+        if (hh < nh) { kind = 0; head = hh; }
+        else if (hh < nh + nkv) { kind = 1; head = hh - nh; }
+        else { kind = 2; head = hh - nh - nkv; }
+    }
+    Row<WT, NCHH> q1, q2;  // prefetched one stage ahead (layer L's rows during layer L-1's down)
+    if (has1) {
+        const LkFusedLayer& l0 = a.layers[0];
+        const LkDevW& w = kind == 0 ? l0.q : (kind == 1 ? l0.k : l0.v);
+        row_issue(q1, w, head * 64 + ip, lane);
+        row_issue(q2, w, head * 64 + ip + 32, lane);
+    }
+
+    LKF_MARK(0);
+    // S0: every block takes the embedding row itself (src/model.rs:200-202).
+    for (uint32_t j = threadIdx.x; j < h; j += FT) xres[j] = lk_embed_elem(a.embed, token, j);
+    __syncthreads();
+    LKF_MARK(1);
+
+    // lm_head: a contiguous row range per block, FLR rows per wave in flight in
+    // each of two register sets
+    const uint32_t V = a.vocab;
+    const uint32_t per_block = (V + gridDim.x - 1) / gridDim.x;
+    const uint32_t r_lo = blockIdx.x * per_block, r_hi = (r_lo + per_block < V) ? r_lo + per_block : V;
+    constexpr int FLR = (WT == LK_Q4_K || NCHH > 1) ? 4 : 8;
+    const uint32_t stride = FW * FLR;
+    const uint32_t r_first = r_lo + (uint32_t)wave * FLR;
+    Row<WT, NCHH> ra[FLR], rb[FLR];
+    auto issue_lm = [&](uint32_t rb0) {
+#pragma unroll
+        for (int k = 0; k < FLR; k++)
+            if (rb0 + k < r_hi) row_issue(ra[k], a.lm_head, rb0 + k, lane);
+    };
+
+    for (uint32_t L = 0; L < nL; L++) {
+        const LkFusedLayer& ly = a.layers[L];
+        const uint32_t ep = base * (nL + 1) + L + 1;
+        const uint32_t par = L & 1;
+        uint64_t* QB = a.qb + (size_t)par * qkvd;
+        uint64_t* PB = a.pb + (size_t)par * nkv * nspan_max * G * 66;  // [j][span][g][66], span stride nspan
+        uint64_t* XP = a.xpb + (size_t)par * h;
+        uint64_t* IB = a.ib + (size_t)par * I;
+        // Weight rows are issued right after a stage's input has arrived, one
+        // or two stages before they are used: vector loads retire in issue
+        // order, so a prefetch issued before a wait would delay that wait.
+        // (The attention stage needs most registers, so only the o_proj row
+        // is held across it.)
+        const uint32_t U5 = I;              // gate/up rows
+        Row<WT, NCHH> orow;                 // issued in S1, used in S4
+        Row<WT, NCHH> gq[3], uq[3];         // issued in S4, used in S5
+        Row<WT, NCHI> dn;                   // issued in S5, used in S6
+        // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
+        if (L > 0) stage_in(c, a.xb + (size_t)par * h, h, ep, xres);
+        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
+        rmsnorm_lds(xres, ly.in_norm, h, a.eps, xin, red);
+        if (has1) {
+            float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
+            float d2 = lk_wave_sum(row_dot(q2, xin, h, lane));
+            if (lane == 0) {
+                const uint32_t r = head * 64 + ip;
+                const float* bias = kind == 0 ? ly.bq : (kind == 1 ? ly.bk : ly.bv);
+                if (bias) {
+                    d1 += bias[r];
+                    d2 += bias[r + 32];
+                }
+                if (kind < 2) rot(d1, d2, __fmul_rn(fpos, a.freq.f[ip]));
+                if (kind == 0) {
+                    publish(QB + r, d1, ep);
+                    publish(QB + r + 32, d2, ep);
+                } else {
+                    KV* cache = (KV*)(kind == 1 ? a.kc : a.vc) + (size_t)L * a.kv_layer +
+                                ((size_t)head * a.max_seq + pos) * 64;
+                    kv_put(cache + ip, d1);
+                    kv_put(cache + ip + 32, d2);
+                    const uint32_t off = qd + (kind == 2 ? kvd : 0) + r;
+                    publish(QB + off, kv_round(d1, KV32), ep);
+                    publish(QB + off + 32, kv_round(d2, KV32), ep);
+                }
+            }
+        }
+        LKF_MARK(2 + 6 * L + 0);
+        // ---------------- S2: attention; unit = (kv head, span of FW tiles), one block
+        for (uint32_t u = blockIdx.x; u < nkv * nspan; u += gridDim.x) {
+            const uint32_t j = u / nspan, sp = u % nspan;
+            LKF_SUB(0);
+            const uint32_t p0 = (sp * FW + (uint32_t)wave) * 64;
+            const bool live = p0 <= pos;
+            const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+            const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+            const uint32_t p = p0 + (uint32_t)lane;
+            const uint32_t sub = (uint32_t)lane >> 3, dq = ((uint32_t)lane & 7) * 8;
+            // cached positions (< pos) do not depend on this token: load them first
+            uint4 kraw[KC], vraw[KC];
+            auto load_v = [&]() {
+#pragma unroll
+                for (int q = 0; q < KC; q++) {
+                    const uint32_t pj = p0 + (uint32_t)(KV32 ? q / 2 : q) * 8 + sub;
+                    const uint32_t dd = dq + (KV32 ? (q & 1) * 4 : 0);
+                    vraw[q] = (live && pj < pos) ? *(const uint4*)(V + (size_t)pj * 64 + dd) : make_uint4(0, 0, 0, 0);
+                }
+            };
+#pragma unroll
+            for (int q = 0; q < KC; q++)
+                kraw[q] = (live && p < pos) ? *(const uint4*)((const uint8_t*)(K + (size_t)p * 64) + 16 * q)
+                                            : make_uint4(0, 0, 0, 0);
+            if constexpr (!KV32) load_v();  // f16: K and V of the tile fit in registers together
+            LKF_SUB(1);
+            // the group's q rows and this token's k, v
+            __syncthreads();
+            for (uint32_t i = threadIdx.x; i < G * 64 + 128; i += FT) {
+                const uint64_t* src = i < G * 64 ? QB + j * G * 64 + i
+                                                 : (i < G * 64 + 64 ? QB + qd + j * 64 + (i - G * 64)
+                                                                    : QB + qd + kvd + j * 64 + (i - G * 64 - 64));
+                qg[i] = await(c, src, ep);
+            }
+            __syncthreads();
+            LKF_SUB(2);
+            if (live) {
+                const bool valid = p <= pos;
+                float s[G];
+#pragma unroll
+                for (int g = 0; g < G; g++) s[g] = 0.f;
+                if (p == pos) {  // this token's k (LDS) packed like a cache row: one code path below
+#pragma unroll
+                    for (int q = 0; q < KC; q++) kraw[q] = pack4(kcur + q * (KV32 ? 4 : 8), KV32);
+                }
+                if (valid) {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {  // 8 elements at a time
+                        float k8[8];
+                        unpack8(kraw, q, KV32, k8);
+#pragma unroll
+                        for (int g = 0; g < G; g++) {
+                            const float4 qa = *(const float4*)(qg + g * 64 + 8 * q);
+                            const float4 qb = *(const float4*)(qg + g * 64 + 8 * q + 4);
+                            float t = s[g];
+                            t = fmaf(k8[0], qa.x, t); t = fmaf(k8[1], qa.y, t);
+                            t = fmaf(k8[2], qa.z, t); t = fmaf(k8[3], qa.w, t);
+                            t = fmaf(k8[4], qb.x, t); t = fmaf(k8[5], qb.y, t);
+                            t = fmaf(k8[6], qb.z, t); t = fmaf(k8[7], qb.w, t);
+                            s[g] = t;
+                        }
+                    }
+                }
+                LKF_SUB(3);
+                if constexpr (KV32) load_v();  // f32: V once the K registers are free
+                float acc[G][8];
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float sg = valid ? s[g] * 0.125f : -INFINITY;
+                    const float m = lk_wave_max(sg);
+                    const float pg = valid ? expf(sg - m) : 0.f;
+                    const float l = lk_wave_sum(pg);
+                    wP[g * 64 + (lane & 7) * 8 + (lane >> 3)] = pg;  // [g][sub][jj]: a lane's 8 are adjacent
+                    if (lane == 0) {
+                        wM[g] = m;
+                        wL[g] = l;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+                }
+                wave_sync_lds();
+                LKF_SUB(6);
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    const uint32_t pj = p0 + jj * 8 + sub;
+                    if (pj == pos) {  // this token's v from LDS, packed like a cache chunk
+                        if constexpr (KV32) {
+                            vraw[2 * jj] = pack4(vcur + dq, true);
+                            vraw[2 * jj + 1] = pack4(vcur + dq + 4, true);
+                        } else {
+                            vraw[jj] = pack4(vcur + dq, false);
+                        }
+                    }
+                    if (pj <= pos) {
+                        float v8[8];
+                        unpack8(vraw, jj, KV32, v8);
+#pragma unroll
+                        for (int g = 0; g < G; g++) {
+                            const float pw = wP[g * 64 + sub * 8 + jj];
+#pragma unroll
+                            for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pw, v8[e], acc[g][e]);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                LKF_SUB(7);
+                // Fold the 4 position groups of each half-wave (row_ror 8, then
+                // an xor-16 swizzle), in three sweeps so the swizzles pipeline.
+#pragma unroll
+                for (int g = 0; g < G; g++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[g][e] += lk_dpp<0x128, 0xF>(acc[g][e], 0.f);
+                float sw[G][8];
+#pragma unroll
+                for (int g = 0; g < G; g++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        sw[g][e] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, acc[g][e]), 0x401F));
+                if ((lane & 31) < 8) {
+#pragma unroll
+                    for (int g = 0; g < G; g++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) wA[((lane >> 5) * G + g) * 64 + dq + e] = acc[g][e] + sw[g][e];
+                }
+            } else {
+                if (lane < G) {
+                    wM[lane] = -INFINITY;
+                    wL[lane] = 0.f;
+                }
+            }
+            __syncthreads();
+            LKF_SUB(4);
+            // fold the FW tiles; one partial (m, l, acc[64]) per query head of the group
+            for (uint32_t t = threadIdx.x; t < G * 64; t += FT) {
+                const uint32_t g = t / 64, d = t % 64;
+                float M = -INFINITY;
+#pragma unroll
+                for (int w2 = 0; w2 < FW; w2++) M = fmaxf(M, wv[w2 * WVF + 3 * G * 64 + g]);
+                float Ls = 0.f, A = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < FW; w2++) {
+                    const float m = wv[w2 * WVF + 3 * G * 64 + g];
+                    if (m != -INFINITY) {
+                        const float sc = expf(m - M);
+                        Ls = fmaf(sc, wv[w2 * WVF + 3 * G * 64 + G + g], Ls);
+                        const float* wa = wv + w2 * WVF + G * 64;  // the wave's two half-wave sums
+                        A = fmaf(sc, wa[g * 64 + d] + wa[(G + g) * 64 + d], A);
+                    }
+                }
+                uint64_t* out = PB + ((size_t)(j * nspan + sp) * G + g) * 66;
+                if (d == 0) {
+                    publish(out, M, ep);
+                    publish(out + 1, Ls, ep);
+                }
+                publish(out + 2 + d, A, ep);
+            }
+            LKF_SUB(5);
+        }
+        LKF_MARK(2 + 6 * L + 1);
+        // ---------------- S4: fold the attention spans + o_proj + residual -> x'
+        {
+            const int u = c.gw;
+            LKF_MARK(2 + 6 * L + 2);
+            stage_in(c, PB, nkv * nspan * G * 66, ep, pbuf);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                const int uu = c.gw + k * c.nw;
+                if (uu < (int)U5) {
+                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
+                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                }
+            }
+            for (uint32_t t = threadIdx.x; t < qd; t += FT) {
+                const uint32_t hq = t / 64, d = t % 64, j = hq / G, g = hq % G;
+                float M = -INFINITY;
+                for (uint32_t sp = 0; sp < nspan; sp++) M = fmaxf(M, pbuf[((j * nspan + sp) * G + g) * 66]);
+                float Ls = 0.f, A = 0.f;
+                for (uint32_t sp = 0; sp < nspan; sp++) {
+                    const float* pp = pbuf + ((j * nspan + sp) * G + g) * 66;
+                    if (pp[0] != -INFINITY) {
+                        const float sc = expf(pp[0] - M);
+                        Ls = fmaf(sc, pp[1], Ls);
+                        A = fmaf(sc, pp[2 + d], A);
+                    }
+                }
+                xin[t] = A / Ls;
+            }
+            __syncthreads();
+            if (u < (int)h) {
+                const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
+                if (lane == 0) publish(XP + u, xres[u] + d, ep);
+            }
+        }
+        LKF_MARK(2 + 6 * L + 3);
+        // ---------------- S5: RMSNorm + gate/up + SwiGLU -> inner
+        {
+            stage_in(c, XP, h, ep, xres);
+            if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
+            if (has1 && L + 1 < nL) {  // the next layer's q/k/v rows
+                const LkFusedLayer& ln = a.layers[L + 1];
+                const LkDevW& w = kind == 0 ? ln.q : (kind == 1 ? ln.k : ln.v);
+                row_issue(q1, w, head * 64 + ip, lane);
+                row_issue(q2, w, head * 64 + ip + 32, lane);
+            }
+            rmsnorm_lds(xres, ly.post_norm, h, a.eps, xin, red);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                const int uu = c.gw + k * c.nw;
+                if (uu < (int)U5) {
+                    const float gg = lk_wave_sum(row_dot(gq[k], xin, h, lane));
+                    const float up = lk_wave_sum(row_dot(uq[k], xin, h, lane));
+                    if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
+                }
+            }
+            for (int uu = c.gw + 3 * c.nw; uu < (int)U5; uu += c.nw) {  // wider than 3 rows per wave
+                Row<WT, NCHH> gr, pr;
+                row_issue(gr, ly.gate, (uint32_t)uu, lane);
+                row_issue(pr, ly.up, (uint32_t)uu, lane);
+                const float gg = lk_wave_sum(row_dot(gr, xin, h, lane));
+                const float up = lk_wave_sum(row_dot(pr, xin, h, lane));
+                if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
+            }
+        }
+        LKF_MARK(2 + 6 * L + 4);
+        // ---------------- S6: down + residual -> x of layer L+1
+        {
+            const uint32_t epn = ep + 1;
+            uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * h;
+            stage_in(c, IB, I, ep, xin);
+            if (c.gw < (int)h) {
+                const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
+                if (lane == 0) publish(XN + c.gw, xres[c.gw] + d, epn);
+            }
+            for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
+                Row<WT, NCHI> rr;
+                row_issue(rr, ly.down, (uint32_t)uu, lane);
+                const float d = lk_wave_sum(row_dot(rr, xin, I, lane));
+                if (lane == 0) publish(XN + uu, xres[uu] + d, epn);
+            }
+        }
+        LKF_MARK(2 + 6 * L + 5);
+    }
+
+    // ---------------- final: RMSNorm + lm_head (double-buffered rows) + argmax keys
+    const uint32_t epf = base * (nL + 1) + nL + 1;
+    uint32_t r0 = r_first;
+    LKF_MARK(2 + 6 * nL);
+    stage_in(c, a.xb + (size_t)(nL & 1) * h, h, epf, xres);
+    issue_lm(r_first);
+    rmsnorm_lds(xres, a.norm, h, a.eps, xin, red);
+    LKF_MARK(2 + 6 * nL + 1);
+    uint64_t best = 0;
+    // every lm_head row meets the same x: this lane's slice of it stays in
+    // registers for the whole loop instead of being re-read from LDS per row
+    float xr[NCHH][ChunkTraits<WT>::elems];
+#pragma unroll
+    for (int i = 0; i < NCHH; i++) {
+        const uint32_t ch = (uint32_t)lane + 64u * i;
+        const bool ok = ch < h / ChunkTraits<WT>::elems;
+        if constexpr (WT == LK_Q4_K) {
+            const uint32_t sb = ch >> 3, k = ch & 7;
+            const float* xl = xin + sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                xr[i][e] = ok ? xl[e] : 0.f;
+                xr[i][16 + e] = ok ? xl[32 + e] : 0.f;
+            }
+        } else {
+            constexpr uint32_t CE = ChunkTraits<WT>::elems;
+#pragma unroll
+            for (int e = 0; e < (int)CE; e++) xr[i][e] = ok ? xin[ch * CE + e] : 0.f;
+        }
+    }
+    auto consume = [&](Row<WT, NCHH>* rr, uint32_t rbase) {
+#pragma unroll
+        for (int k = 0; k < FLR; k++) {
+            if (rbase + k < r_hi) {
+                const float v = lk_wave_sum(row_dot_reg(rr[k], xr, h, lane));
+                if (lane == 0) {
+                    a.logits[rbase + k] = v;
+                    const uint64_t kk = lk_argmax_key(v, rbase + k);
+                    best = kk > best ? kk : best;
+                }
+            }
+        }
+    };
+    while (r0 < r_hi) {
+        uint32_t r1 = r0 + stride;
+#pragma unroll
+        for (int k = 0; k < FLR; k++)
+            if (r1 + k < r_hi) row_issue(rb[k], a.lm_head, r1 + k, lane);
+        consume(ra, r0);
+        r0 = r1;
+        if (r0 >= r_hi) break;
+        r1 = r0 + stride;
+#pragma unroll
+        for (int k = 0; k < FLR; k++)
+            if (r1 + k < r_hi) row_issue(ra[k], a.lm_head, r1 + k, lane);
+        consume(rb, r0);
+        r0 = r1;
+    }
+    __shared__ uint64_t bk[FW];
+    if (lane == 0) bk[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = bk[0];
+        for (int w2 = 1; w2 < FW; w2++) b = bk[w2] > b ? bk[w2] : b;
+        uint64_t* kw = a.kb + 2 * blockIdx.x;
+        __hip_atomic_store(kw, ((uint64_t)epf << 32) | (b >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(kw + 1, ((uint64_t)epf << 32) | (b & 0xFFFFFFFFu), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    LKF_MARK(2 + 6 * nL + 2);
+    if (blockIdx.x != 0 || wave != 0) return;
+    // block 0, wave 0: fold every block's key, then advance the step
+    uint64_t b = 0;
+    for (uint32_t i0 = 0; i0 < 2 * gridDim.x; i0 += 8 * 64) {  // eight words per lane in flight
+        uint64_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t i = i0 + (uint32_t)(k / 2) * 128 + 2 * (uint32_t)lane + (uint32_t)(k & 1);
+            w[k] = i < 2 * gridDim.x ? ld_word(a.kb + i) : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const uint32_t i = i0 + (uint32_t)(k / 2) * 128 + 2 * (uint32_t)lane;
+            if (i < 2 * gridDim.x) {
+                const uint32_t hi = (uint32_t)(w[k] >> 32) == epf ? (uint32_t)w[k]
+                                                                  : __float_as_uint(await(c, a.kb + i, epf));
+                const uint32_t lo = (uint32_t)(w[k + 1] >> 32) == epf ? (uint32_t)w[k + 1]
+                                                                      : __float_as_uint(await(c, a.kb + i + 1, epf));
+                const uint64_t kk = ((uint64_t)hi << 32) | lo;
+                b = kk > b ? kk : b;
+            }
+        }
+    }
+#pragma unroll
+    for (int m2 = 32; m2 >= 1; m2 >>= 1) {
+        const uint64_t o = __shfl_xor(b, m2, 64);
+        b = o > b ? o : b;
+    }
+    if (lane == 0) {
+        const uint32_t tok = lk_argmax_idx(b);
+        LkStepState s = st;
+        if (s.n_feed > 0) {
+            s.token = a.feed[s.fed];
+            s.fed += 1;
+            s.n_feed -= 1;
+        } else {
+            if (a.ids_out) a.ids_out[s.n_out] = tok;
+            s.n_out += 1;
+            s.token = tok;
+        }
+        s.pos += 1;
+        *a.st = s;
+        a.epoch[0] = base + 1;
+        if (a.trace && a.trace_block == 0) a.trace[2 + 6 * nL + 3] = __builtin_amdgcn_s_memrealtime();
+    }
+}
+
+}  // namespace lkf
+
+size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks) {
+    uint32_t vmax = I > h ? I : h;
+    if (nh * 64 > vmax) vmax = nh * 64;
+    const size_t nspan_max = (max_chunks + FW - 1) / FW;
+    return ((size_t)vmax + h + 16 + (size_t)G * 64 + 128 + (size_t)FW * (3 * G * 64 + 2 * G) +
+            (size_t)nkv * nspan_max * G * 66) * 4;
+}
+int lk_fused_threads() { return FT; }
+
+template <int WT, int NCHH, int NCHI, typename KV, int G>
+static hipError_t launch_t(const LkFusedArgs& a, unsigned blocks, size_t lds, hipStream_t st, bool setup) {
+    auto kfn = lkf::fused_step_kernel<WT, NCHH, NCHI, KV, G>;
+    if (setup) {
+        hipError_t e = hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        int nb = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kfn, FT, lds);
+        if (e != hipSuccess) return e;
+        return nb >= 1 ? hipSuccess : hipErrorInvalidConfiguration;
+    }
+    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(FT), lds, st, a);
+    return hipGetLastError();
+}
+
+// Instantiated shapes: (weight type, 16-byte chunks per lane for rows of
+// hidden / intermediate width, KV cache type, GQA group).
+#define LKF_SHAPES(X)                        \
+    X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */  \
+    X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */  \
+    X(LK_Q4_K, 1, 3, 8)  /* TinyLlama-1.1B */
+
+hipError_t lk_fused_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, int kv_f32, unsigned blocks,
+                           size_t lds, hipStream_t st, bool setup) {
+#define X(T, NH, NI, GG)                                                                             \
+    if (wt == T && nchh == NH && nchi == NI && G == GG) {                                            \
+        return kv_f32 ? launch_t<T, NH, NI, float, GG>(a, blocks, lds, st, setup)                   \
+                      : launch_t<T, NH, NI, uint16_t, GG>(a, blocks, lds, st, setup);              \
+    }
+    LKF_SHAPES(X)
+#undef X
+    return hipErrorNotSupported;
+}

@@ -15,14 +15,40 @@ enum LkType : uint32_t { LK_F32 = 0, LK_F16 = 1, LK_Q8_0 = 8, LK_Q4_K = 12 };
 // src/gguf/dequant.rs:135-137).
 __device__ __forceinline__ float lk_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
+// Wave-64 reductions on the DPP network (no LDS round trips): quad_perm
+// pairs, row_ror 4 / 8 give every lane its 16-lane row total, row_bcast 15 /
+// 31 carry the row totals up to lane 63, whose value is broadcast.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float lk_dpp(float v, float old) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                   __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF,
+                                                                   false));
+}
 __device__ __forceinline__ float lk_wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, LK_WAVE);
-    return v;
+    v += lk_dpp<0xB1, 0xF>(v, 0.f);   // quad_perm [1,0,3,2]
+    v += lk_dpp<0x4E, 0xF>(v, 0.f);   // quad_perm [2,3,0,1]
+    v += lk_dpp<0x124, 0xF>(v, 0.f);  // row_ror 4
+    v += lk_dpp<0x128, 0xF>(v, 0.f);  // row_ror 8
+    v += lk_dpp<0x142, 0xA>(v, 0.f);  // row_bcast 15
+    v += lk_dpp<0x143, 0xC>(v, 0.f);  // row_bcast 31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 __device__ __forceinline__ float lk_wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, LK_WAVE));
+    const float ninf = -INFINITY;
+    v = fmaxf(v, lk_dpp<0xB1, 0xF>(v, ninf));
+    v = fmaxf(v, lk_dpp<0x4E, 0xF>(v, ninf));
+    v = fmaxf(v, lk_dpp<0x124, 0xF>(v, ninf));
+    v = fmaxf(v, lk_dpp<0x128, 0xF>(v, ninf));
+    v = fmaxf(v, lk_dpp<0x142, 0xA>(v, ninf));
+    v = fmaxf(v, lk_dpp<0x143, 0xC>(v, ninf));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// Sum over the four lanes {l, l^8, l^16 .. within one 32-lane half}: row_ror 8
+// then an xor-16 swizzle.  Lane l of each half then holds the sum of the four
+// lanes of that half with the same (l & 7).
+__device__ __forceinline__ float lk_half_sum_mod8(float v) {
+    v += lk_dpp<0x128, 0xF>(v, 0.f);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
     return v;
 }
 

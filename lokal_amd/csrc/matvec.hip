@@ -54,35 +54,6 @@ hipError_t lk_matvec_launch(const LkMvArgs& a, int mode, hipStream_t st, LkMvPla
     }
 }
 
-// One element of a weight row, exactly as dequant_row_ref computes it
-// (src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K).
-__device__ __forceinline__ float dequant_elem(const LkDevW& w, uint32_t r, uint32_t j) {
-    if (w.type == LK_F16) {
-        return lk_h2f(((const uint16_t*)w.data)[(size_t)r * w.cols + j]);
-    } else if (w.type == LK_Q8_0) {
-        const int8_t q = ((const int8_t*)w.data)[(size_t)r * w.cols + j];
-        const float d = lk_h2f(((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + j / 32]);
-        return __fmul_rn((float)q, d);
-    } else if (w.type == LK_Q4_K) {
-        const uint32_t nsb = w.cols / 256, sb = j / 256, e = j % 256;
-        const uint8_t* hdr = w.aux + ((size_t)r * nsb + sb) * 16;
-        const uint8_t* qs = w.data + ((size_t)r * nsb + sb) * 128;
-        const float d = lk_h2f((uint16_t)(hdr[0] | (hdr[1] << 8)));
-        const float dmin = lk_h2f((uint16_t)(hdr[2] | (hdr[3] << 8)));
-        const uint32_t grp = e / 64, within = e % 64, hi = within / 32, l = within % 32;
-        const uint32_t is = 2 * grp + hi;
-        const uint32_t* s = (const uint32_t*)(hdr + 4);
-        uint32_t sc, m;
-        lk::scale_min_k4(is, s[0], s[1], s[2], sc, m);
-        const uint8_t byte = qs[grp * 32 + l];
-        const uint32_t q = hi ? (byte >> 4) : (byte & 0x0F);
-        const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
-        return __fsub_rn(__fmul_rn(d1, (float)q), m1);
-    } else {  // F32
-        return ((const float*)w.data)[(size_t)r * w.cols + j];
-    }
-}
-
 // out[i, :] = dequant(row(i)); row(i) = ids[i] when ids is given, else row0 + i.
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const LkDevW w, const uint32_t* __restrict__ ids,
                                                            uint32_t row0, uint32_t nrows, float* __restrict__ out) {
@@ -91,7 +62,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const LkDevW w, const
     if (i >= nrows || j >= w.cols) return;
     const uint32_t r = ids ? ids[i] : row0 + i;
     if (r >= w.rows) return;
-    out[(size_t)i * w.cols + j] = dequant_elem(w, r, j);
+    out[(size_t)i * w.cols + j] = lk_embed_elem(w, r, j);
 }
 
 hipError_t lk_dequant_launch(const LkDevW& w, uint32_t row0, uint32_t nrows, float* out, hipStream_t st) {
@@ -115,7 +86,7 @@ __global__ __launch_bounds__(256) void embed_step_kernel(const LkDevW w, const L
     const uint32_t j = blockIdx.x * 256 + threadIdx.x;
     const uint32_t r = st->token;
     if (j >= w.cols || r >= w.rows) return;
-    x[j] = dequant_elem(w, r, j);
+    x[j] = lk_embed_elem(w, r, j);
 }
 
 hipError_t lk_embed_step_launch(const LkDevW& table, const LkStepState* st_dev, float* x, hipStream_t st) {

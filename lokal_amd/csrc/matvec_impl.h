@@ -122,6 +122,38 @@ __device__ __forceinline__ float dot_q4k(uint4 q, uint4 hdr, uint32_t k, const f
     return lo_part + hi_part;
 }
 
+// One element of a weight row, exactly as dequant_row_ref computes it
+// (src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K).
+}  // namespace lk
+__device__ __forceinline__ float lk_embed_elem(const LkDevW& w, uint32_t r, uint32_t j) {
+    if (w.type == LK_F16) {
+        return lk_h2f(((const uint16_t*)w.data)[(size_t)r * w.cols + j]);
+    } else if (w.type == LK_Q8_0) {
+        const int8_t q = ((const int8_t*)w.data)[(size_t)r * w.cols + j];
+        const float d = lk_h2f(((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + j / 32]);
+        return __fmul_rn((float)q, d);
+    } else if (w.type == LK_Q4_K) {
+        const uint32_t nsb = w.cols / 256, sb = j / 256, e = j % 256;
+        const uint8_t* hdr = w.aux + ((size_t)r * nsb + sb) * 16;
+        const uint8_t* qs = w.data + ((size_t)r * nsb + sb) * 128;
+        const float d = lk_h2f((uint16_t)(hdr[0] | (hdr[1] << 8)));
+        const float dmin = lk_h2f((uint16_t)(hdr[2] | (hdr[3] << 8)));
+        const uint32_t grp = e / 64, within = e % 64, hi = within / 32, l = within % 32;
+        const uint32_t is = 2 * grp + hi;
+        const uint32_t* s = (const uint32_t*)(hdr + 4);
+        uint32_t sc, m;
+        lk::scale_min_k4(is, s[0], s[1], s[2], sc, m);
+        const uint8_t byte = qs[grp * 32 + l];
+        const uint32_t q = hi ? (byte >> 4) : (byte & 0x0F);
+        const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
+        return __fsub_rn(__fmul_rn(d1, (float)q), m1);
+    } else {  // F32
+        return ((const float*)w.data)[(size_t)r * w.cols + j];
+    }
+}
+
+namespace lk {
+
 template <int WT>
 __device__ __forceinline__ size_t row_data_bytes(uint32_t cols) {
     if constexpr (WT == LK_Q8_0) return cols;
