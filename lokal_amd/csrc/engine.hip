@@ -437,6 +437,9 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
     }
     if (e->lm_head->dw.type == LKHIP_F32)
         return fail(LKHIP_E_UNSUPPORTED, "lm_head must be F16, Q8_0 or Q4_K on the hip backend");
+    if (!lk_lm_head_fits(e->lm_head->dw.type, cfg->hidden_size))
+        return fail(LKHIP_E_UNSUPPORTED, "hidden_size %u is wider than the lm_head kernel takes for type %s",
+                    cfg->hidden_size, type_name(e->lm_head->dw.type));
     e->matvec_bytes += e->lm_head->bytes;
     if ((rc = fused_setup(e.get()))) return rc;
     *out = e.release();
@@ -462,17 +465,17 @@ struct lkhip_session {
     hipStream_t stream = nullptr;
     DevBuf kc, vc;  // [layer][n_kv][max_seq][64], f16 or f32 (kv_f32)
     int kv_f32 = 0;
-    DevBuf x, xn, qkv, att, inner, logits, part, keys, state, feed, ids_out;
+    DevBuf x, xn, qkv, att, inner, logits, part, keys, head_epoch, err, state, feed, ids_out;
     LkStepState* h_state = nullptr;  // pinned
     float* h_logits = nullptr;       // pinned
-    uint32_t n_keys = 0;
+    uint32_t head_blocks = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     // one-kernel decode step: exchange buffers, epoch counter, error flag
     bool use_fused = false;
     uint32_t max_chunks = 0;
     size_t fused_lds = 0;
-    DevBuf xb, qb, pb, ab, xpb, ib, kb, epoch, err;
+    DevBuf xb, qb, pb, ab, xpb, ib, epoch;
     DevBuf trace;          // stage timestamps of one block (lkhip_session_set_trace)
     int trace_block = -1;
     // profiling
@@ -517,6 +520,27 @@ static LkMvArgs mv_args(const float* x, uint32_t cols) {
     return a;
 }
 
+// Final RMSNorm + lm_head + argmax + step advance (lmhead.hip).
+static hipError_t enqueue_head(lkhip_session* s, const float* x, uint32_t x_stride, hipStream_t st) {
+    const lkhip_engine* e = s->e;
+    LkHeadArgs a{};
+    a.x = x;
+    a.x_stride = x_stride;
+    a.norm = e->norm.as<float>();
+    a.eps = e->cfg.rms_norm_eps;
+    a.w = e->lm_head->dw;
+    a.h = e->cfg.hidden_size;
+    a.vocab = e->cfg.vocab_size;
+    a.logits = s->logits.as<float>();
+    a.keys = s->keys.as<uint64_t>();
+    a.epoch = s->head_epoch.as<uint32_t>();
+    a.err = s->err.as<uint32_t>();
+    a.st = s->state.as<LkStepState>();
+    a.feed = s->feed.as<uint32_t>();
+    a.ids_out = s->ids_out.as<uint32_t>();
+    return lk_lm_head_launch(a, s->head_blocks, st);
+}
+
 // The whole decode step of one token (Model::forward, src/model.rs:196-262)
 // enqueued on the session stream; reads token/pos from the device state.
 static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
@@ -540,7 +564,6 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.layers = e->fused_layers.as<LkFusedLayer>();
         a.n_layers = c.num_hidden_layers;
         a.embed = e->embed->dw;
-        a.lm_head = e->lm_head->dw;
         a.norm = e->norm.as<float>();
         a.freq = e->freq;
         a.h = h;
@@ -557,23 +580,22 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.st = state;
         a.epoch = s->epoch.as<uint32_t>();
         a.err = s->err.as<uint32_t>();
-        a.feed = s->feed.as<uint32_t>();
-        a.ids_out = s->ids_out.as<uint32_t>();
-        a.logits = s->logits.as<float>();
         a.xb = s->xb.as<uint64_t>();
         a.qb = s->qb.as<uint64_t>();
         a.pb = s->pb.as<uint64_t>();
         a.ab = s->ab.as<uint64_t>();
         a.xpb = s->xpb.as<uint64_t>();
         a.ib = s->ib.as<uint64_t>();
-        a.kb = s->kb.as<uint64_t>();
         a.trace = s->trace_block >= 0 ? s->trace.as<uint64_t>() : nullptr;
         a.trace_block = (uint32_t)(s->trace_block >= 0 ? s->trace_block : 0);
-        // The one kernel streams every matvec weight of the step: its time is
-        // the dequant-matvec time of the token.
+        // The one kernel streams every layer weight of the step: its time is
+        // the dequant-matvec time of the layers.
         STEP(lk_fused_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, s->kv_f32,
                              e->fused_blocks, s->fused_lds, st, false),
-             C_MATVEC, e->matvec_bytes);
+             C_MATVEC, e->matvec_bytes - e->lm_head->bytes);
+        // the last layer's output: f32 halves of the (f32 | epoch) words
+        STEP(enqueue_head(s, (const float*)(s->xb.as<uint64_t>() + (size_t)(c.num_hidden_layers & 1) * h), 2, st),
+             C_LMHEAD, e->lm_head->bytes);
         return hipSuccess;
     }
 
@@ -638,18 +660,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             STEP(lk_matvec_launch(a, LK_MV_ACC, st), C_MATVEC, ly.down->bytes);
         }
     }
-    STEP(lk_rmsnorm_launch(x, e->norm.as<float>(), 1, h, c.rms_norm_eps, xn, st), C_OTHER, 0);
-    {
-        LkMvArgs a = mv_args(xn, h);
-        a.nseg = 1;
-        a.seg[0] = {e->lm_head->dw, nullptr, s->logits.as<float>()};
-        a.total_rows = c.vocab_size;
-        a.keys = s->keys.as<uint64_t>();
-        STEP(lk_matvec_launch(a, LK_MV_ARGMAX, st), C_LMHEAD, e->lm_head->bytes);
-    }
-    STEP(lk_step_finish_launch(s->keys.as<uint64_t>(), s->n_keys, state, s->feed.as<uint32_t>(),
-                               s->ids_out.as<uint32_t>(), st),
-         C_OTHER, 0);
+    STEP(enqueue_head(s, x, 1, st), C_LMHEAD, e->lm_head->bytes);
 #undef STEP
     return hipSuccess;
 }
@@ -696,8 +707,10 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         (rc = dev_alloc(s->logits, (size_t)c.vocab_size * 4)))
         return rc;
     if ((rc = dev_alloc(s->part, lk_attn_part_floats(1, c.num_attention_heads, (uint32_t)max_seq) * 4))) return rc;
-    s->n_keys = lk_matvec_plan(e->lm_head->dw.type, c.vocab_size, c.hidden_size, LK_MV_ARGMAX).blocks;
-    if ((rc = dev_alloc(s->keys, (size_t)s->n_keys * 8))) return rc;
+    s->head_blocks = lk_lm_head_blocks(c.vocab_size, e->lm_head->dw.type, c.hidden_size);
+    if ((rc = dev_alloc(s->keys, (size_t)LK_HEAD_MAX_BLOCKS * 2 * 8)) || (rc = dev_alloc(s->head_epoch, 4)) ||
+        (rc = dev_alloc(s->err, 4)))
+        return rc;
     if ((rc = dev_alloc(s->state, sizeof(LkStepState)))) return rc;
     if ((rc = dev_alloc(s->feed, max_seq * 4)) || (rc = dev_alloc(s->ids_out, max_seq * 4))) return rc;
     if (e->fused_ok && max_seq <= LK_FUSED_MAX_SEQ) {
@@ -707,8 +720,8 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
             (rc = dev_alloc(s->pb, 2 * (size_t)c.num_key_value_heads * s->max_chunks * G * 66 * 8)) ||
             (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
-            (rc = dev_alloc(s->ib, 2 * I * 8)) || (rc = dev_alloc(s->kb, (size_t)e->fused_blocks * 2 * 8)) ||
-            (rc = dev_alloc(s->epoch, 4)) || (rc = dev_alloc(s->err, 4)))
+            (rc = dev_alloc(s->ib, 2 * I * 8)) ||
+            (rc = dev_alloc(s->epoch, 4)))
             return rc;
         const uint32_t one = 1;
         HIP_OR_FAIL(hipMemcpy(s->epoch.p, &one, 4, hipMemcpyHostToDevice));
@@ -795,10 +808,14 @@ static int check_tok(lkhip_session* s, uint32_t token, size_t pos) {
 // timed out, the session drops to the per-stage kernels and the call fails.
 static int sync_check(lkhip_session* s) {
     HIP_OR_FAIL(hipStreamSynchronize(s->stream));
-    if (!s->use_fused) return LKHIP_OK;
     uint32_t flag = 0;
     HIP_OR_FAIL(hipMemcpy(&flag, s->err.p, 4, hipMemcpyDeviceToHost));
     if (!flag) return LKHIP_OK;
+    if (flag & 2) {
+        HIP_OR_FAIL(hipMemset(s->err.p, 0, 4));
+        return fail(LKHIP_E_HIP, "the lm_head launch timed out collecting its workgroups' argmax keys (is every CU "
+                                 "free?) — the token and state of that step are invalid; restart from a known position");
+    }
     s->use_fused = false;
     if (s->exec) {
         (void)hipGraphExecDestroy(s->exec);

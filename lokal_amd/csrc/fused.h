@@ -14,7 +14,7 @@ struct LkFusedLayer {
 struct LkFusedArgs {
     const LkFusedLayer* layers;  // device array, n_layers entries
     uint32_t n_layers;
-    LkDevW embed, lm_head;
+    LkDevW embed;
     const float* norm;
     LkFreq freq;
     uint32_t h, I, nh, nkv, vocab;
@@ -27,9 +27,6 @@ struct LkFusedArgs {
     LkStepState* st;
     uint32_t* epoch;     // token counter of the exchange epochs
     uint32_t* err;       // set when a bounded wait timed out
-    const uint32_t* feed;
-    uint32_t* ids_out;
-    float* logits;
     // exchange buffers of (f32 | epoch) words, two copies by layer parity
     uint64_t* xb;   // [2][h]        layer input x
     uint64_t* qb;   // [2][qd+2kvd]  rotated q, this token's k and v
@@ -37,16 +34,15 @@ struct LkFusedArgs {
     uint64_t* ab;   // [2][qd]       attention output
     uint64_t* xpb;  // [2][h]        x after the attention residual
     uint64_t* ib;   // [2][I]        SwiGLU output
-    uint64_t* kb;   // [blocks][2]   argmax keys
     // optional stage timestamps (s_memrealtime, 100 MHz) of one block:
     // [0] start, [1] after the embedding, [2 + 6L + s] after stage s of layer
-    // L, then after the final norm, after lm_head, and (block 0) at the end
+    // L, then at the end of the block
     uint64_t* trace;
     uint32_t trace_block;
 };
 // ... followed by 8 sub-steps of layer 1's attention stage (when the traced
 // block runs an attention unit there).
-inline size_t lk_fused_trace_len(uint32_t n_layers) { return 2 + 6 * (size_t)n_layers + 4 + 8; }
+inline size_t lk_fused_trace_len(uint32_t n_layers) { return 2 + 6 * (size_t)n_layers + 1 + 8; }
 
 // LDS of one workgroup for sessions of up to max_chunks 64-position tiles.
 size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks);

@@ -26,8 +26,8 @@
 //   S4 o_proj   folds the span partials of every head in LDS, o_proj + residual -> x'
 //   S5 gate/up  RMSNorm(x') + SwiGLU  -> inner
 //   S6 down     + residual            -> x of the next layer
-//   final       RMSNorm + lm_head (+ logits, rows double-buffered) + argmax
-//               keys; block 0 folds them and advances the step state.
+// The final RMSNorm + lm_head + argmax is the next launch (lmhead.hip): the
+// 145 MB lm_head stream wants 4 blocks per CU, this kernel holds one.
 // Weight rows of a stage are issued one stage early (o_proj with gate/up,
 // gate/up with down, down with the next layer's q/k/v).
 // Every wait is bounded: on timeout the kernel raises an error flag, stops
@@ -44,7 +44,7 @@
 #define LKF_SUB(k)                                                                    \
     do {                                                                              \
         if (L == 1 && a.trace && blockIdx.x == a.trace_block && threadIdx.x == 0)     \
-            a.trace[2 + 6 * nL + 4 + (k)] = __builtin_amdgcn_s_memrealtime();         \
+            a.trace[2 + 6 * nL + 1 + (k)] = __builtin_amdgcn_s_memrealtime();         \
     } while (0)
 #define LKF_MARK(k)                                                          \
     do {                                                                     \
@@ -138,89 +138,6 @@ __device__ __forceinline__ void rmsnorm_lds(const float* xr, const float* __rest
     const float scale = 1.0f / sqrtf(tot / (float)n + eps);
     for (uint32_t i = threadIdx.x; i < n; i += FT) xo[i] = __fmul_rn(__fmul_rn(xr[i], scale), g[i]);
     __syncthreads();
-}
-
-// One weight row held in registers: its 16-byte chunks for this lane.
-template <int WT, int NCH>
-struct Row {
-    uint4 q[NCH];
-    uint4 hd[NCH];  // Q4_K super-block heads
-    uint32_t d[NCH];  // Q8_0 block scales, raw f16 bits: converted at use, so issuing never waits
-};
-
-template <int WT>
-__device__ __forceinline__ const uint8_t* row_ptr(const LkDevW& w, uint32_t r) {
-    return w.data + (size_t)r * row_data_bytes<WT>(w.cols);
-}
-template <int WT>
-__device__ __forceinline__ const uint8_t* aux_ptr(const LkDevW& w, uint32_t r) {
-    return w.aux + (size_t)r * row_aux_bytes<WT>(w.cols);
-}
-
-template <int WT, int NCH>
-__device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint32_t r, int lane) {
-    const uint32_t nchunk = w.cols / ChunkTraits<WT>::elems;
-    const uint8_t* rp = row_ptr<WT>(w, r);
-    const uint8_t* ap = aux_ptr<WT>(w, r);
-#pragma unroll
-    for (int i = 0; i < NCH; i++) {
-        const uint32_t ch = (uint32_t)lane + 64u * i;
-        const bool ok = ch < nchunk;
-        R.q[i] = ok ? ld_stream16(rp + 16u * ch) : make_uint4(0, 0, 0, 0);
-        if constexpr (WT == LK_Q8_0) R.d[i] = ok ? (uint32_t)((const uint16_t*)ap)[ch >> 1] : 0u;
-        if constexpr (WT == LK_Q4_K) R.hd[i] = ok ? *(const uint4*)(ap + 16u * (ch >> 3)) : make_uint4(0, 0, 0, 0);
-    }
-}
-
-// This lane's partial dot of the row with x (LDS); reduce across the wave after.
-template <int WT, int NCH>
-__device__ __forceinline__ float row_dot(const Row<WT, NCH>& R, const float* x, uint32_t cols, int lane) {
-    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < NCH; i++) {
-        const uint32_t ch = (uint32_t)lane + 64u * i;
-        if (ch < nchunk) {
-            if constexpr (WT == LK_Q8_0) {
-                acc = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], x + ch * 16), acc);
-            } else if constexpr (WT == LK_F16) {
-                acc += dot_f16(R.q[i], x + ch * 8);
-            } else {
-                const uint32_t sb = ch >> 3, k = ch & 7;
-                acc += dot_q4k(R.q[i], R.hd[i], k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
-            }
-        }
-    }
-    return acc;
-}
-
-// row_dot with this lane's x slice already in registers (xr[i] = the x values
-// chunk i of the lane multiplies; Q4_K: 16 low-nibble then 16 high-nibble values).
-template <int WT, int NCH>
-__device__ __forceinline__ float row_dot_reg(const Row<WT, NCH>& R, const float (&xr)[NCH][ChunkTraits<WT>::elems],
-                                             uint32_t cols, int lane) {
-    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < NCH; i++) {
-        const uint32_t ch = (uint32_t)lane + 64u * i;
-        if (ch < nchunk) {
-            if constexpr (WT == LK_Q8_0) {
-                acc = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], xr[i]), acc);
-            } else if constexpr (WT == LK_F16) {
-                acc += dot_f16(R.q[i], xr[i]);
-            } else {
-                float xx[64];  // dot_q4k reads x[0..15] and x[32..47]
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    xx[e] = xr[i][e];
-                    xx[32 + e] = xr[i][16 + e];
-                }
-                acc += dot_q4k(R.q[i], R.hd[i], ch & 7, xx);
-            }
-        }
-    }
-    return acc;
 }
 
 __device__ __forceinline__ float kv_round(float v, bool f32) {
@@ -342,21 +259,6 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     for (uint32_t j = threadIdx.x; j < h; j += FT) xres[j] = lk_embed_elem(a.embed, token, j);
     __syncthreads();
     LKF_MARK(1);
-
-    // lm_head: a contiguous row range per block, FLR rows per wave in flight in
-    // each of two register sets
-    const uint32_t V = a.vocab;
-    const uint32_t per_block = (V + gridDim.x - 1) / gridDim.x;
-    const uint32_t r_lo = blockIdx.x * per_block, r_hi = (r_lo + per_block < V) ? r_lo + per_block : V;
-    constexpr int FLR = (WT == LK_Q4_K || NCHH > 1) ? 4 : 8;
-    const uint32_t stride = FW * FLR;
-    const uint32_t r_first = r_lo + (uint32_t)wave * FLR;
-    Row<WT, NCHH> ra[FLR], rb[FLR];
-    auto issue_lm = [&](uint32_t rb0) {
-#pragma unroll
-        for (int k = 0; k < FLR; k++)
-            if (rb0 + k < r_hi) row_issue(ra[k], a.lm_head, rb0 + k, lane);
-    };
 
     for (uint32_t L = 0; L < nL; L++) {
         const LkFusedLayer& ly = a.layers[L];
@@ -649,121 +551,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         LKF_MARK(2 + 6 * L + 5);
     }
 
-    // ---------------- final: RMSNorm + lm_head (double-buffered rows) + argmax keys
-    const uint32_t epf = base * (nL + 1) + nL + 1;
-    uint32_t r0 = r_first;
+    // The final RMSNorm, lm_head and argmax run in the next launch
+    // (lmhead.hip); every block has read `base`, so the epoch may advance.
     LKF_MARK(2 + 6 * nL);
-    stage_in(c, a.xb + (size_t)(nL & 1) * h, h, epf, xres);
-    issue_lm(r_first);
-    rmsnorm_lds(xres, a.norm, h, a.eps, xin, red);
-    LKF_MARK(2 + 6 * nL + 1);
-    uint64_t best = 0;
-    // every lm_head row meets the same x: this lane's slice of it stays in
-    // registers for the whole loop instead of being re-read from LDS per row
-    float xr[NCHH][ChunkTraits<WT>::elems];
-#pragma unroll
-    for (int i = 0; i < NCHH; i++) {
-        const uint32_t ch = (uint32_t)lane + 64u * i;
-        const bool ok = ch < h / ChunkTraits<WT>::elems;
-        if constexpr (WT == LK_Q4_K) {
-            const uint32_t sb = ch >> 3, k = ch & 7;
-            const float* xl = xin + sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                xr[i][e] = ok ? xl[e] : 0.f;
-                xr[i][16 + e] = ok ? xl[32 + e] : 0.f;
-            }
-        } else {
-            constexpr uint32_t CE = ChunkTraits<WT>::elems;
-#pragma unroll
-            for (int e = 0; e < (int)CE; e++) xr[i][e] = ok ? xin[ch * CE + e] : 0.f;
-        }
-    }
-    auto consume = [&](Row<WT, NCHH>* rr, uint32_t rbase) {
-#pragma unroll
-        for (int k = 0; k < FLR; k++) {
-            if (rbase + k < r_hi) {
-                const float v = lk_wave_sum(row_dot_reg(rr[k], xr, h, lane));
-                if (lane == 0) {
-                    a.logits[rbase + k] = v;
-                    const uint64_t kk = lk_argmax_key(v, rbase + k);
-                    best = kk > best ? kk : best;
-                }
-            }
-        }
-    };
-    while (r0 < r_hi) {
-        uint32_t r1 = r0 + stride;
-#pragma unroll
-        for (int k = 0; k < FLR; k++)
-            if (r1 + k < r_hi) row_issue(rb[k], a.lm_head, r1 + k, lane);
-        consume(ra, r0);
-        r0 = r1;
-        if (r0 >= r_hi) break;
-        r1 = r0 + stride;
-#pragma unroll
-        for (int k = 0; k < FLR; k++)
-            if (r1 + k < r_hi) row_issue(ra[k], a.lm_head, r1 + k, lane);
-        consume(rb, r0);
-        r0 = r1;
-    }
-    __shared__ uint64_t bk[FW];
-    if (lane == 0) bk[wave] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t b = bk[0];
-        for (int w2 = 1; w2 < FW; w2++) b = bk[w2] > b ? bk[w2] : b;
-        uint64_t* kw = a.kb + 2 * blockIdx.x;
-        __hip_atomic_store(kw, ((uint64_t)epf << 32) | (b >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(kw + 1, ((uint64_t)epf << 32) | (b & 0xFFFFFFFFu), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    LKF_MARK(2 + 6 * nL + 2);
-    if (blockIdx.x != 0 || wave != 0) return;
-    // block 0, wave 0: fold every block's key, then advance the step
-    uint64_t b = 0;
-    for (uint32_t i0 = 0; i0 < 2 * gridDim.x; i0 += 8 * 64) {  // eight words per lane in flight
-        uint64_t w[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const uint32_t i = i0 + (uint32_t)(k / 2) * 128 + 2 * (uint32_t)lane + (uint32_t)(k & 1);
-            w[k] = i < 2 * gridDim.x ? ld_word(a.kb + i) : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-            const uint32_t i = i0 + (uint32_t)(k / 2) * 128 + 2 * (uint32_t)lane;
-            if (i < 2 * gridDim.x) {
-                const uint32_t hi = (uint32_t)(w[k] >> 32) == epf ? (uint32_t)w[k]
-                                                                  : __float_as_uint(await(c, a.kb + i, epf));
-                const uint32_t lo = (uint32_t)(w[k + 1] >> 32) == epf ? (uint32_t)w[k + 1]
-                                                                      : __float_as_uint(await(c, a.kb + i + 1, epf));
-                const uint64_t kk = ((uint64_t)hi << 32) | lo;
-                b = kk > b ? kk : b;
-            }
-        }
-    }
-#pragma unroll
-    for (int m2 = 32; m2 >= 1; m2 >>= 1) {
-        const uint64_t o = __shfl_xor(b, m2, 64);
-        b = o > b ? o : b;
-    }
-    if (lane == 0) {
-        const uint32_t tok = lk_argmax_idx(b);
-        LkStepState s = st;
-        if (s.n_feed > 0) {
-            s.token = a.feed[s.fed];
-            s.fed += 1;
-            s.n_feed -= 1;
-        } else {
-            if (a.ids_out) a.ids_out[s.n_out] = tok;
-            s.n_out += 1;
-            s.token = tok;
-        }
-        s.pos += 1;
-        *a.st = s;
-        a.epoch[0] = base + 1;
-        if (a.trace && a.trace_block == 0) a.trace[2 + 6 * nL + 3] = __builtin_amdgcn_s_memrealtime();
-    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch[0] = base + 1;
 }
 
 }  // namespace lkf

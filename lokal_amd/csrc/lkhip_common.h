@@ -139,6 +139,30 @@ hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const 
 hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepState* st_dev,
                                  const uint32_t* feed_ids, uint32_t* ids_out, hipStream_t st);
 
+// End of a decode step in one launch (lmhead.hip): final RMSNorm, lm_head,
+// argmax, step-state advance.
+#define LK_HEAD_MAX_BLOCKS 1024u
+struct LkHeadArgs {
+    const float* x;      // residual stream before the final norm
+    uint32_t x_stride;   // floats between elements (2: f32 halves of (f32 | epoch) words)
+    const float* norm;
+    float eps;
+    LkDevW w;
+    uint32_t h, vocab;
+    float* logits;
+    uint64_t* keys;      // 2 * LK_HEAD_MAX_BLOCKS words of (epoch | key half)
+    uint32_t* epoch;     // launches so far (advanced by block 0)
+    uint32_t* err;       // set to 2 if the key wait timed out
+    LkStepState* st;
+    const uint32_t* feed;
+    uint32_t* ids_out;
+};
+// lm_head rows of up to 256 16-byte chunks (Q8_0: h <= 4096, F16: 2048, Q4_K: 8192)
+bool lk_lm_head_fits(uint32_t type, uint32_t h);
+uint32_t lk_lm_head_rows(uint32_t type, uint32_t h);
+uint32_t lk_lm_head_blocks(uint32_t vocab, uint32_t type, uint32_t h);
+hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t st);
+
 // Attention (attention.hip).  q rows of n_heads*64, caches f16
 // [seq][n_kv][max_seq][64]; ctx from ctx_len[seq] or, when null, st_dev->pos+1.
 struct LkAttnArgs {

@@ -167,6 +167,100 @@ __device__ __forceinline__ size_t row_aux_bytes(uint32_t cols) {
     else return (size_t)(cols / 256) * 16;
 }
 
+// One weight row held in registers: its 16-byte chunks for this lane.
+template <int WT, int NCH>
+struct Row {
+    uint4 q[NCH];
+    uint4 hd[NCH];  // Q4_K super-block heads
+    uint32_t d[NCH];  // Q8_0 block scales, raw f16 bits: converted at use, so issuing never waits
+};
+
+template <int WT>
+__device__ __forceinline__ const uint8_t* row_ptr(const LkDevW& w, uint32_t r) {
+    return w.data + (size_t)r * row_data_bytes<WT>(w.cols);
+}
+template <int WT>
+__device__ __forceinline__ const uint8_t* aux_ptr(const LkDevW& w, uint32_t r) {
+    return w.aux + (size_t)r * row_aux_bytes<WT>(w.cols);
+}
+
+// Issues the row's loads.  Every lane loads (lanes past the row end reload
+// chunk 0 and their products are dropped in row_dot): a lane-dependent branch
+// here would let the compiler pull the scale conversion, and with it a wait
+// for the load, into the branch, serialising the rows of a batch.
+template <int WT, int NCH>
+__device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint32_t r, int lane) {
+    const uint32_t nchunk = w.cols / ChunkTraits<WT>::elems;
+    const uint8_t* rp = row_ptr<WT>(w, r);
+    const uint8_t* ap = aux_ptr<WT>(w, r);
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch0 = (uint32_t)lane + 64u * i;
+        const uint32_t ch = ch0 < nchunk ? ch0 : 0u;
+        R.q[i] = ld_stream16(rp + 16u * ch);
+        if constexpr (WT == LK_Q8_0) R.d[i] = (uint32_t)((const uint16_t*)ap)[ch >> 1];
+        if constexpr (WT == LK_Q4_K) R.hd[i] = *(const uint4*)(ap + 16u * (ch >> 3));
+    }
+}
+
+// This lane's partial dot of the row with x (LDS); reduce across the wave after.
+// Straight-line: lanes past the row end compute on chunk 0 and drop the term.
+template <int WT, int NCH>
+__device__ __forceinline__ float row_dot(const Row<WT, NCH>& R, const float* x, uint32_t cols, int lane) {
+    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch0 = (uint32_t)lane + 64u * i;
+        const bool ok = ch0 < nchunk;
+        const uint32_t ch = ok ? ch0 : 0u;
+        float t;
+        if constexpr (WT == LK_Q8_0) {
+            const float s = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], x + ch * 16), acc);
+            acc = ok ? s : acc;
+            continue;
+        } else if constexpr (WT == LK_F16) {
+            t = dot_f16(R.q[i], x + ch * 8);
+        } else {
+            const uint32_t sb = ch >> 3, k = ch & 7;
+            t = dot_q4k(R.q[i], R.hd[i], k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
+        }
+        acc += ok ? t : 0.f;
+    }
+    return acc;
+}
+
+// row_dot with this lane's x slice already in registers (xr[i] = the x values
+// chunk i of the lane multiplies; Q4_K: 16 low-nibble then 16 high-nibble values).
+template <int WT, int NCH>
+__device__ __forceinline__ float row_dot_reg(const Row<WT, NCH>& R, const float (&xr)[NCH][ChunkTraits<WT>::elems],
+                                             uint32_t cols, int lane) {
+    const uint32_t nchunk = cols / ChunkTraits<WT>::elems;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch = (uint32_t)lane + 64u * i;
+        float t;
+        if constexpr (WT == LK_Q8_0) {
+            const float s = fmaf(lk_h2f((uint16_t)R.d[i]), dot_q8(R.q[i], xr[i]), acc);
+            acc = ch < nchunk ? s : acc;
+            continue;
+        } else if constexpr (WT == LK_F16) {
+            t = dot_f16(R.q[i], xr[i]);
+        } else {
+            float xx[64];  // dot_q4k reads x[0..15] and x[32..47]
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                xx[e] = xr[i][e];
+                xx[32 + e] = xr[i][16 + e];
+            }
+            t = dot_q4k(R.q[i], R.hd[i], ch & 7, xx);
+        }
+        acc += ch < nchunk ? t : 0.f;
+    }
+    return acc;
+}
+
 template <int WT, int NCH, int R, int MODE>
 __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
     constexpr int NR = (MODE == LK_MV_SWIGLU) ? 2 * R : R;

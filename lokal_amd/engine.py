@@ -171,18 +171,18 @@ class Session:
         check(lib().lkhip_session_set_trace(self._h, int(block)))
 
     def stage_times_us(self) -> dict:
-        """Stage durations (us) of the last one-kernel step, for the traced block."""
-        n = 2 + 6 * self.engine.cfg.num_hidden_layers + 4 + 8  # stage marks, then attention sub-steps
+        """Stage durations (us) of the last one-kernel step, for the traced block
+        (the final norm + lm_head + argmax is a separate launch, not traced)."""
+        L = self.engine.cfg.num_hidden_layers
+        n = 2 + 6 * L + 1 + 8  # stage marks, end of block, then attention sub-steps
         t = np.zeros(n, dtype=np.uint64)
         check(lib().lkhip_session_trace(self._h, t.ctypes.data_as(C.POINTER(C.c_uint64)), n))
         t = t[:n - 8]
         us = np.diff(t.astype(np.float64)) / 100.0  # 100 MHz counter
-        L = self.engine.cfg.num_hidden_layers
         names = ["qkv", "attn", "merge", "o_proj", "gate_up", "down"]
         per = us[1:1 + 6 * L].reshape(L, 6)
         return {"embed": float(us[0]), **{n_: per[:, i].tolist() for i, n_ in enumerate(names)},
-                "final_norm": float(us[1 + 6 * L]), "lm_head": float(us[2 + 6 * L]),
-                "argmax": float(us[3 + 6 * L]), "total": float((t[-1] - t[0]) / 100.0)}
+                "end": float(us[1 + 6 * L]), "total": float((t[-1] - t[0]) / 100.0)}
 
     def close(self):
         if self._h:

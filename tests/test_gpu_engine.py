@@ -23,6 +23,14 @@ from lokal_amd.config import ModelConfig
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
+# End to end over many steps with an f16 KV cache: each cached element is
+# rounded to 11 significant bits, and the two summation orders (GPU and CPU)
+# can round an element near a rounding midpoint to neighbouring f16 values, a
+# 2^-11 relative step that sharp attention passes on to the logits nearly
+# undamped.  The long greedy runs therefore allow two such ulps over TOL
+# (measured worst case at the Qwen shape: 1.2e-3 after 62 steps; 4e-5 with
+# an f32 cache, which is held to TOL).
+TOL_F16_KV = TOL + 2.0 ** -10
 
 
 def rel_err(got, want):
@@ -194,8 +202,9 @@ def _greedy_identity(name, kv, prompt_len=16, steps=64, seed=0, allow_near_tie=F
     s, o = eng.session(max_seq, kv_dtype=kv), om.session(max_seq, kv_f16=(kv == "f16"))
     lg = s.prefill(prompt)
     lo = o.prefill(prompt)
+    tol = TOL_F16_KV if kv == "f16" else TOL
     print(f"{name}/{kv}: prefill logits rel err {rel_err(lg, lo):.3g}")
-    assert rel_err(lg, lo) < TOL
+    assert rel_err(lg, lo) < tol
     first = int(oracle.argmax(lo))
     assert int(np.argmax(lg)) == first
     gpu_ids = [first] + list(s.decode_greedy(first, prompt_len, steps - 1))
@@ -225,9 +234,9 @@ def _greedy_identity(name, kv, prompt_len=16, steps=64, seed=0, allow_near_tie=F
         ref_i = cpu_logits[i]
         err = rel_err(lg_i, ref_i)
         gap = float(np.sort(ref_i)[-1] - np.sort(ref_i)[-2])
-        band = 2 * TOL * float(np.max(np.abs(ref_i)))
+        band = 2 * tol * float(np.max(np.abs(ref_i)))
         print(f"{name}/{kv}: step {i}: logits rel err {err:.3g}, CPU top-2 gap {gap:.4g}, tolerance band {band:.4g}")
-        assert err < TOL and gap < band, "divergence is not a near-tie within tolerance"
+        assert err < tol and gap < band, "divergence is not a near-tie within tolerance"
         r.close()
     s.close()
     eng.close()
@@ -244,6 +253,6 @@ def test_greedy_64_steps_identical_to_cpu_path_f32_kv(name):
 def test_greedy_64_steps_identical_with_f16_kv(name):
     """The GPU path's f16 KV cache against the CPU path storing K/V through f16.
     Identical ids, except that a divergence is accepted at a step whose logits
-    agree within 1e-3 and whose top-2 gap lies inside that band: with f16
-    K/V, a one-ulp rounding flip can reorder such a near-tie."""
+    agree within TOL_F16_KV and whose top-2 gap lies inside that band: with
+    f16 K/V, a one-ulp rounding flip can reorder such a near-tie."""
     _greedy_identity(name, "f16", allow_near_tie=True)
