@@ -179,6 +179,7 @@ int lkhip_malloc(void** dptr, size_t bytes);
 int lkhip_free(void* dptr);
 int lkhip_memcpy_htod(void* dst, const void* src, size_t bytes);
 int lkhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int lkhip_memcpy_dtod(void* dst, const void* src, size_t bytes);
 int lkhip_memset(void* dptr, int value, size_t bytes);
 int lkhip_synchronize(void);
 /* Streams at default priority and events for timing kernel-level calls. */

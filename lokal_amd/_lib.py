@@ -89,6 +89,7 @@ SIGNATURES = {
     "lkhip_free": (C.c_int, [_P]),
     "lkhip_memcpy_htod": (C.c_int, [_P, _P, C.c_size_t]),
     "lkhip_memcpy_dtoh": (C.c_int, [_P, _P, C.c_size_t]),
+    "lkhip_memcpy_dtod": (C.c_int, [_P, _P, C.c_size_t]),
     "lkhip_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
     "lkhip_synchronize": (C.c_int, []),
     "lkhip_stream_create": (C.c_int, [C.POINTER(_P)]),

@@ -1052,6 +1052,10 @@ extern "C" int lkhip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
     HIP_OR_FAIL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return LKHIP_OK;
 }
+extern "C" int lkhip_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+    HIP_OR_FAIL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return LKHIP_OK;
+}
 extern "C" int lkhip_memset(void* p, int v, size_t bytes) {
     HIP_OR_FAIL(hipMemset(p, v, bytes));
     return LKHIP_OK;
