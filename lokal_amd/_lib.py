@@ -1,14 +1,16 @@
 """ctypes view of liblokal_hip.so (include/lokal_hip.h).
 
-The library is loaded from this package directory; if it is missing the
-import fails loudly -- there is no CPU fallback behind this API.
+The library is loaded from this package directory (or from $LOKAL_HIP_LIB,
+to compare builds); if it is missing the import fails loudly -- there is no
+CPU fallback behind this API.
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "liblokal_hip.so"
+LIB_PATH = Path(os.environ.get("LOKAL_HIP_LIB") or Path(__file__).resolve().parent / "liblokal_hip.so")
 
 LKHIP_OK = 0
 LKHIP_F32, LKHIP_F16, LKHIP_Q8_0, LKHIP_Q4_K = 0, 1, 8, 12

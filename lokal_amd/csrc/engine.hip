@@ -324,6 +324,10 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "more rows per stage than waves";
         return LKHIP_OK;
     }
+    if (c.num_attention_heads * LK_FUSED_PARTS > nw) {
+        e->fused_why = "more attention items than waves";
+        return LKHIP_OK;
+    }
     // LDS limit for the longest session the one-kernel step serves
     e->fused_lds = lk_fused_lds_bytes(h, I, c.num_attention_heads, c.num_key_value_heads, (uint32_t)e->fused_g,
                                       (LK_FUSED_MAX_SEQ + 63) / 64);
@@ -714,11 +718,11 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
     if ((rc = dev_alloc(s->state, sizeof(LkStepState)))) return rc;
     if ((rc = dev_alloc(s->feed, max_seq * 4)) || (rc = dev_alloc(s->ids_out, max_seq * 4))) return rc;
     if (e->fused_ok && max_seq <= LK_FUSED_MAX_SEQ) {
-        const size_t h = c.hidden_size, I = c.intermediate_size, G = (size_t)e->fused_g;
+        const size_t h = c.hidden_size, I = c.intermediate_size;
         const size_t qkvd = e->qd + 2 * e->kvd;
         s->max_chunks = (uint32_t)((max_seq + 63) / 64);
         if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
-            (rc = dev_alloc(s->pb, 2 * (size_t)c.num_key_value_heads * s->max_chunks * G * 66 * 8)) ||
+            (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * std::min(s->max_chunks, LK_FUSED_PARTS) * 66 * 8)) ||
             (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
             (rc = dev_alloc(s->ib, 2 * I * 8)) ||
             (rc = dev_alloc(s->epoch, 4)))

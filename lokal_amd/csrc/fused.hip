@@ -20,10 +20,11 @@
 //   S1 QKV      RMSNorm(x) + q/k/v rows in (i, i+32) pairs + bias + RoPE;
 //               k/v rounded to the cache type, written to the KV cache and
 //               published for this token's attention
-//   S2 attn     one workgroup per (kv head, span of 8 x 64 positions):
-//               flash-decoding over the span, K/V of cached positions loaded
-//               before the wait for q; one (m, l, acc) partial per query head
-//   S4 o_proj   folds the span partials of every head in LDS, o_proj + residual -> x'
+//   S2 attn     one wave per (query head, chunk of 64-position tiles), spread
+//               over the whole grid: K/V of cached positions loaded before the
+//               wait for q; online softmax; one (m, l, acc[64]) partial each
+//   S3 merge    one wave per query head folds its chunks -> attention output
+//   S4 o_proj   o_proj + residual -> x'
 //   S5 gate/up  RMSNorm(x') + SwiGLU  -> inner
 //   S6 down     + residual            -> x of the next layer
 // The final RMSNorm + lm_head + argmax is the next launch (lmhead.hip): the
@@ -36,7 +37,7 @@
 #include "matvec_impl.h"
 #include "fused.h"
 
-#define FW 8
+#define FW ((int)LK_FUSED_WAVES)
 #define FT (FW * 64)
 #define FCH 64
 // Stage timestamp of the traced block (thread 0 only).
@@ -208,21 +209,16 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
     const uint32_t vmax = (I > h ? I : h) > qd ? (I > h ? I : h) : qd;
-    const uint32_t nspan_max = (a.max_chunks + FW - 1) / FW;
-    constexpr uint32_t WVF = 3 * G * 64 + 2 * G;  // P [G][64], acc [2 halves][G][64], m [G], l [G]
     float* xin = lds;                 // vmax: the (normalised) input vector of a stage
     float* xres = xin + vmax;         // h: the residual stream of this layer
     float* red = xres + h;            // 16: block reductions
-    float* qg = red + 16;             // G*64 + 128: the group's q rows, this token's k and v
-    float* wv = qg + G * 64 + 128;    // FW * WVF: per wave P tile, acc, m, l
-    float* pbuf = wv + FW * WVF;      // nkv * nspan_max * G * 66: attention partials
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* wP = wv + wave * WVF;      // [G][64]
-    float* wA = wP + G * 64;          // [G][64]
-    float* wM = wA + 2 * G * 64;      // [G]
-    float* wL = wM + G;               // [G]
-    float* kcur = qg + G * 64;
-    float* vcur = kcur + 64;
+    float* wv = red + 16;             // FW * 256: per wave q, this token's k and v, P
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: stage branches stay scalar
+    float* wq = wv + wave * 256;      // [64] the query head's q
+    float* wk = wq + 64;              // [64] this token's k (the chunk holding pos)
+    float* wvc = wk + 64;             // [64] this token's v
+    float* wP = wvc + 64;             // [64] softmax weights of a tile, [group][jj] order
 
     Ctx c{&a, a.err, lane, wave, (int)(wave * gridDim.x + blockIdx.x), (int)(FW * gridDim.x)};
     constexpr bool KV32 = sizeof(KV) == 4;
@@ -233,7 +229,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     const uint32_t nL = a.n_layers;
     const float fpos = (float)pos;
     const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
-    const uint32_t nspan = (ntile + FW - 1) / FW;   // one attention unit = FW tiles of one kv head
+    // attention items: (query head, chunk of TPW consecutive tiles), one wave each
+    const uint32_t TPW = (ntile + LK_FUSED_PARTS - 1) / LK_FUSED_PARTS;
+    const uint32_t nch = (ntile + TPW - 1) / TPW;   // chunks per head, <= LK_FUSED_PARTS and <= max_chunks
+    const uint32_t nps = a.max_chunks < LK_FUSED_PARTS ? a.max_chunks : LK_FUSED_PARTS;  // partial slots per head
 
     // S1 work of this wave: q/k/v rows (i, i+32) of one head
     const uint32_t U1 = (nh + 2 * nkv) * 32;
@@ -265,7 +264,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         const uint32_t ep = base * (nL + 1) + L + 1;
         const uint32_t par = L & 1;
         uint64_t* QB = a.qb + (size_t)par * qkvd;
-        uint64_t* PB = a.pb + (size_t)par * nkv * nspan_max * G * 66;  // [j][span][g][66], span stride nspan
+        uint64_t* PB = a.pb + (size_t)par * nh * nps * 66;  // [head][chunk][m, l, acc[64]]
+        uint64_t* AB = a.ab + (size_t)par * qd;
         uint64_t* XP = a.xpb + (size_t)par * h;
         uint64_t* IB = a.ib + (size_t)par * I;
         // Weight rows are issued right after a stage's input has arrived, one
@@ -307,171 +307,184 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
         }
         LKF_MARK(2 + 6 * L + 0);
-        // ---------------- S2: attention; unit = (kv head, span of FW tiles), one block
-        for (uint32_t u = blockIdx.x; u < nkv * nspan; u += gridDim.x) {
-            const uint32_t j = u / nspan, sp = u % nspan;
+        // ---------------- S2: attention partials.  Item = (query head, chunk of
+        // TPW tiles of 64 positions), one wave each, spread over the grid: a
+        // wave scores 64 positions at a time (lane = position), keeps an
+        // online softmax over its tiles and accumulates P.V with lane =
+        // (position group lane & 7, dims 8 * (lane >> 3) ..+7).
+        if (c.gw < (int)(nh * nch)) {
+            const uint32_t hq = (uint32_t)c.gw / nch, ck = (uint32_t)c.gw % nch;
+            const uint32_t j = hq / G;
+            const uint32_t t0 = ck * TPW, t1 = (t0 + TPW < ntile) ? t0 + TPW : ntile;
+            const bool has_cur = t1 == ntile;  // the chunk holding position pos
             LKF_SUB(0);
-            const uint32_t p0 = (sp * FW + (uint32_t)wave) * 64;
-            const bool live = p0 <= pos;
             const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
             const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
-            const uint32_t p = p0 + (uint32_t)lane;
-            const uint32_t sub = (uint32_t)lane >> 3, dq = ((uint32_t)lane & 7) * 8;
-            // cached positions (< pos) do not depend on this token: load them first
+            const uint32_t plast = pos > 0 ? pos - 1 : 0;
+            const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
+            // cached positions (< pos) do not depend on this token.  Straight-line
+            // loads: positions >= pos read a clamped (valid) row, replaced or masked below.
             uint4 kraw[KC], vraw[KC];
-            auto load_v = [&]() {
+            auto load_k = [&](uint32_t t) {
+                const uint32_t p = t * 64 + (uint32_t)lane;
+                const uint32_t pk = p < pos ? p : plast;
+#pragma unroll
+                for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)(K + pk * 64u) + 16 * q);
+            };
+            auto load_v = [&](uint32_t t) {
 #pragma unroll
                 for (int q = 0; q < KC; q++) {
-                    const uint32_t pj = p0 + (uint32_t)(KV32 ? q / 2 : q) * 8 + sub;
+                    const uint32_t pj = t * 64 + (uint32_t)(KV32 ? q / 2 : q) * 8 + sub;
                     const uint32_t dd = dq + (KV32 ? (q & 1) * 4 : 0);
-                    vraw[q] = (live && pj < pos) ? *(const uint4*)(V + (size_t)pj * 64 + dd) : make_uint4(0, 0, 0, 0);
+                    vraw[q] = *(const uint4*)(V + ((pj < pos ? pj : plast) * 64u + dd));
                 }
             };
-#pragma unroll
-            for (int q = 0; q < KC; q++)
-                kraw[q] = (live && p < pos) ? *(const uint4*)((const uint8_t*)(K + (size_t)p * 64) + 16 * q)
-                                            : make_uint4(0, 0, 0, 0);
-            if constexpr (!KV32) load_v();  // f16: K and V of the tile fit in registers together
+            // f16: a tile's K and V fit in registers together; f32: V follows the scores
+            auto load_tile = [&](uint32_t t) {
+                load_k(t);
+                if constexpr (!KV32) load_v(t);
+            };
+            load_tile(t0);
             LKF_SUB(1);
-            // the group's q rows and this token's k, v
-            __syncthreads();
-            for (uint32_t i = threadIdx.x; i < G * 64 + 128; i += FT) {
-                const uint64_t* src = i < G * 64 ? QB + j * G * 64 + i
-                                                 : (i < G * 64 + 64 ? QB + qd + j * 64 + (i - G * 64)
-                                                                    : QB + qd + kvd + j * 64 + (i - G * 64 - 64));
-                qg[i] = await(c, src, ep);
-            }
-            __syncthreads();
-            LKF_SUB(2);
-            if (live) {
-                const bool valid = p <= pos;
-                float s[G];
-#pragma unroll
-                for (int g = 0; g < G; g++) s[g] = 0.f;
-                if (p == pos) {  // this token's k (LDS) packed like a cache row: one code path below
-#pragma unroll
-                    for (int q = 0; q < KC; q++) kraw[q] = pack4(kcur + q * (KV32 ? 4 : 8), KV32);
+            {  // this head's q; this token's k and v for the chunk that holds pos
+                const uint64_t* sq = QB + hq * 64 + lane;
+                const uint64_t* sk = QB + qd + j * 64 + lane;
+                const uint64_t* sv = QB + qd + kvd + j * 64 + lane;
+                const uint64_t w0 = ld_word(sq);
+                const uint64_t w1 = has_cur ? ld_word(sk) : 0;
+                const uint64_t w2 = has_cur ? ld_word(sv) : 0;
+                wq[lane] = (uint32_t)(w0 >> 32) == ep ? __uint_as_float((uint32_t)w0) : await(c, sq, ep);
+                if (has_cur) {
+                    wk[lane] = (uint32_t)(w1 >> 32) == ep ? __uint_as_float((uint32_t)w1) : await(c, sk, ep);
+                    wvc[lane] = (uint32_t)(w2 >> 32) == ep ? __uint_as_float((uint32_t)w2) : await(c, sv, ep);
                 }
-                if (valid) {
+            }
+            wave_sync_lds();
+            LKF_SUB(2);
+            float m = -INFINITY, l = 0.f, acc[8];
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {  // 8 elements at a time
-                        float k8[8];
-                        unpack8(kraw, q, KV32, k8);
+            for (int e = 0; e < 8; e++) acc[e] = 0.f;
+            for (uint32_t t = t0; t < t1; t++) {
+                if (t > t0) load_tile(t);
+                const uint32_t p = t * 64 + (uint32_t)lane;
+                const bool valid = p <= pos;
+                if (p == pos) {  // this token's k packed like a cache row: one code path below
 #pragma unroll
-                        for (int g = 0; g < G; g++) {
-                            const float4 qa = *(const float4*)(qg + g * 64 + 8 * q);
-                            const float4 qb = *(const float4*)(qg + g * 64 + 8 * q + 4);
-                            float t = s[g];
-                            t = fmaf(k8[0], qa.x, t); t = fmaf(k8[1], qa.y, t);
-                            t = fmaf(k8[2], qa.z, t); t = fmaf(k8[3], qa.w, t);
-                            t = fmaf(k8[4], qb.x, t); t = fmaf(k8[5], qb.y, t);
-                            t = fmaf(k8[6], qb.z, t); t = fmaf(k8[7], qb.w, t);
-                            s[g] = t;
-                        }
-                    }
+                    for (int q = 0; q < KC; q++) kraw[q] = pack4(wk + q * (KV32 ? 4 : 8), KV32);
+                }
+                float s = 0.f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {  // 8 dims at a time
+                    float k8[8];
+                    unpack8(kraw, q, KV32, k8);
+                    const float4 qa = *(const float4*)(wq + 8 * q);
+                    const float4 qb = *(const float4*)(wq + 8 * q + 4);
+                    s = fmaf(k8[0], qa.x, s); s = fmaf(k8[1], qa.y, s);
+                    s = fmaf(k8[2], qa.z, s); s = fmaf(k8[3], qa.w, s);
+                    s = fmaf(k8[4], qb.x, s); s = fmaf(k8[5], qb.y, s);
+                    s = fmaf(k8[6], qb.z, s); s = fmaf(k8[7], qb.w, s);
                 }
                 LKF_SUB(3);
-                if constexpr (KV32) load_v();  // f32: V once the K registers are free
-                float acc[G][8];
+                if constexpr (KV32) load_v(t);
+                // online softmax over the chunk's tiles (the split-invariant form
+                // of math::softmax, src/math.rs:55-66)
+                const float sg = valid ? s * 0.125f : -INFINITY;
+                const float mn = fmaxf(m, lk_wave_max(sg));
+                const float pe = valid ? expf(sg - mn) : 0.f;
+                const float rs = expf(m - mn);  // 0 on the first tile
+                l = fmaf(l, rs, lk_wave_sum(pe));
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float sg = valid ? s[g] * 0.125f : -INFINITY;
-                    const float m = lk_wave_max(sg);
-                    const float pg = valid ? expf(sg - m) : 0.f;
-                    const float l = lk_wave_sum(pg);
-                    wP[g * 64 + (lane & 7) * 8 + (lane >> 3)] = pg;  // [g][sub][jj]: a lane's 8 are adjacent
-                    if (lane == 0) {
-                        wM[g] = m;
-                        wL[g] = l;
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-                }
+                for (int e = 0; e < 8; e++) acc[e] *= rs;
+                m = mn;
+                wP[(lane & 7) * 8 + (lane >> 3)] = pe;  // [group][jj]: a lane's 8 weights are adjacent
                 wave_sync_lds();
-                LKF_SUB(6);
+                LKF_SUB(4);
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) {
-                    const uint32_t pj = p0 + jj * 8 + sub;
+                    const uint32_t pj = t * 64 + jj * 8 + sub;
                     if (pj == pos) {  // this token's v from LDS, packed like a cache chunk
                         if constexpr (KV32) {
-                            vraw[2 * jj] = pack4(vcur + dq, true);
-                            vraw[2 * jj + 1] = pack4(vcur + dq + 4, true);
+                            vraw[2 * jj] = pack4(wvc + dq, true);
+                            vraw[2 * jj + 1] = pack4(wvc + dq + 4, true);
                         } else {
-                            vraw[jj] = pack4(vcur + dq, false);
+                            vraw[jj] = pack4(wvc + dq, false);
                         }
                     }
                     if (pj <= pos) {
                         float v8[8];
                         unpack8(vraw, jj, KV32, v8);
+                        const float pw = wP[sub * 8 + jj];
 #pragma unroll
-                        for (int g = 0; g < G; g++) {
-                            const float pw = wP[g * 64 + sub * 8 + jj];
-#pragma unroll
-                            for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pw, v8[e], acc[g][e]);
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                LKF_SUB(7);
-                // Fold the 4 position groups of each half-wave (row_ror 8, then
-                // an xor-16 swizzle), in three sweeps so the swizzles pipeline.
-#pragma unroll
-                for (int g = 0; g < G; g++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[g][e] += lk_dpp<0x128, 0xF>(acc[g][e], 0.f);
-                float sw[G][8];
-#pragma unroll
-                for (int g = 0; g < G; g++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        sw[g][e] = __builtin_bit_cast(
-                            float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, acc[g][e]), 0x401F));
-                if ((lane & 31) < 8) {
-#pragma unroll
-                    for (int g = 0; g < G; g++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) wA[((lane >> 5) * G + g) * 64 + dq + e] = acc[g][e] + sw[g][e];
-                }
-            } else {
-                if (lane < G) {
-                    wM[lane] = -INFINITY;
-                    wL[lane] = 0.f;
-                }
-            }
-            __syncthreads();
-            LKF_SUB(4);
-            // fold the FW tiles; one partial (m, l, acc[64]) per query head of the group
-            for (uint32_t t = threadIdx.x; t < G * 64; t += FT) {
-                const uint32_t g = t / 64, d = t % 64;
-                float M = -INFINITY;
-#pragma unroll
-                for (int w2 = 0; w2 < FW; w2++) M = fmaxf(M, wv[w2 * WVF + 3 * G * 64 + g]);
-                float Ls = 0.f, A = 0.f;
-#pragma unroll
-                for (int w2 = 0; w2 < FW; w2++) {
-                    const float m = wv[w2 * WVF + 3 * G * 64 + g];
-                    if (m != -INFINITY) {
-                        const float sc = expf(m - M);
-                        Ls = fmaf(sc, wv[w2 * WVF + 3 * G * 64 + G + g], Ls);
-                        const float* wa = wv + w2 * WVF + G * 64;  // the wave's two half-wave sums
-                        A = fmaf(sc, wa[g * 64 + d] + wa[(G + g) * 64 + d], A);
+                        for (int e = 0; e < 8; e++) acc[e] = fmaf(pw, v8[e], acc[e]);
                     }
                 }
-                uint64_t* out = PB + ((size_t)(j * nspan + sp) * G + g) * 66;
-                if (d == 0) {
-                    publish(out, M, ep);
-                    publish(out + 1, Ls, ep);
-                }
-                publish(out + 2 + d, A, ep);
+                wave_sync_lds();  // wP is rewritten by the next tile
             }
             LKF_SUB(5);
+            // Sum the 8 position groups of each dims chunk (8 adjacent lanes):
+            // quad_perm pairs, quad halves, then row_ror 4 (lane l takes lane
+            // l-4 of its row), after which lanes 4..7 of each 8 hold the total.
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float v = acc[e];
+                v += lk_dpp<0xB1, 0xF>(v, 0.f);
+                v += lk_dpp<0x4E, 0xF>(v, 0.f);
+                v += lk_dpp<0x124, 0xF>(v, 0.f);
+                acc[e] = v;
+            }
+            uint64_t* out = PB + ((size_t)hq * nps + ck) * 66;
+            if (lane == 0) {
+                publish(out, m, ep);
+                publish(out + 1, l, ep);
+            }
+            if ((lane & 7) == 4) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) publish(out + 2 + dq + e, acc[e], ep);
+            }
+            LKF_SUB(6);
         }
         LKF_MARK(2 + 6 * L + 1);
-        // ---------------- S4: fold the attention spans + o_proj + residual -> x'
+        // ---------------- S3: merge each head's chunks -> attention output (lane = dim)
+        if (c.gw < (int)nh) {
+            const uint32_t hq = (uint32_t)c.gw;
+            const uint64_t* pp = PB + (size_t)hq * nps * 66;
+            float M = -INFINITY, Ls = 0.f, A = 0.f;
+            for (uint32_t k0 = 0; k0 < nch; k0 += 4) {  // four chunks' loads in flight at once
+                uint64_t w[12];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const bool ok = k0 + k < nch;
+                    const uint64_t* q0 = pp + (k0 + k) * 66;
+                    w[3 * k] = ok ? ld_word(q0) : 0;
+                    w[3 * k + 1] = ok ? ld_word(q0 + 1) : 0;
+                    w[3 * k + 2] = ok ? ld_word(q0 + 2 + lane) : 0;
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (k0 + k < nch) {
+                        const uint64_t* q0 = pp + (k0 + k) * 66;
+                        const uint64_t* src[3] = {q0, q0 + 1, q0 + 2 + lane};
+                        float v[3];
+#pragma unroll
+                        for (int i = 0; i < 3; i++)
+                            v[i] = (uint32_t)(w[3 * k + i] >> 32) == ep ? __uint_as_float((uint32_t)w[3 * k + i])
+                                                                        : await(c, src[i], ep);
+                        // (m, l, acc) folded online: rescale to the larger max
+                        const float Mn = fmaxf(M, v[0]);
+                        const float so = expf(M - Mn), sn = expf(v[0] - Mn);
+                        Ls = fmaf(Ls, so, sn * v[1]);
+                        A = fmaf(A, so, sn * v[2]);
+                        M = Mn;
+                    }
+                }
+            }
+            publish(AB + hq * 64 + lane, A / Ls, ep);
+        }
+        LKF_MARK(2 + 6 * L + 2);
+        // ---------------- S4: o_proj + residual -> x'
         {
             const int u = c.gw;
-            LKF_MARK(2 + 6 * L + 2);
-            stage_in(c, PB, nkv * nspan * G * 66, ep, pbuf);
+            stage_in(c, AB, qd, ep, xin);
 #pragma unroll
             for (int k = 0; k < 3; k++) {
                 const int uu = c.gw + k * c.nw;
@@ -480,22 +493,6 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     row_issue(uq[k], ly.up, (uint32_t)uu, lane);
                 }
             }
-            for (uint32_t t = threadIdx.x; t < qd; t += FT) {
-                const uint32_t hq = t / 64, d = t % 64, j = hq / G, g = hq % G;
-                float M = -INFINITY;
-                for (uint32_t sp = 0; sp < nspan; sp++) M = fmaxf(M, pbuf[((j * nspan + sp) * G + g) * 66]);
-                float Ls = 0.f, A = 0.f;
-                for (uint32_t sp = 0; sp < nspan; sp++) {
-                    const float* pp = pbuf + ((j * nspan + sp) * G + g) * 66;
-                    if (pp[0] != -INFINITY) {
-                        const float sc = expf(pp[0] - M);
-                        Ls = fmaf(sc, pp[1], Ls);
-                        A = fmaf(sc, pp[2 + d], A);
-                    }
-                }
-                xin[t] = A / Ls;
-            }
-            __syncthreads();
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
                 if (lane == 0) publish(XP + u, xres[u] + d, ep);
@@ -560,11 +557,12 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
 }  // namespace lkf
 
 size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks) {
+    (void)nkv;
+    (void)G;
+    (void)max_chunks;
     uint32_t vmax = I > h ? I : h;
     if (nh * 64 > vmax) vmax = nh * 64;
-    const size_t nspan_max = (max_chunks + FW - 1) / FW;
-    return ((size_t)vmax + h + 16 + (size_t)G * 64 + 128 + (size_t)FW * (3 * G * 64 + 2 * G) +
-            (size_t)nkv * nspan_max * G * 66) * 4;
+    return ((size_t)vmax + h + 16 + (size_t)FW * 256) * 4;
 }
 int lk_fused_threads() { return FT; }
 
