@@ -324,6 +324,10 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "more rows per stage than waves";
         return LKHIP_OK;
     }
+    if (h > LK_FUSED_MAX_H || c.num_hidden_layers > LK_FUSED_MAX_LAYERS) {
+        e->fused_why = "wider or deeper than the one-kernel step takes";
+        return LKHIP_OK;
+    }
     if (c.num_attention_heads * LK_FUSED_PARTS > nw) {
         e->fused_why = "more attention items than waves";
         return LKHIP_OK;

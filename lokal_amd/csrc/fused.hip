@@ -40,17 +40,17 @@
 #define FW ((int)LK_FUSED_WAVES)
 #define FT (FW * 64)
 #define FCH 64
-// Stage timestamp of the traced block (thread 0 only).
-// Sub-steps of layer 1's attention unit (traced block, thread 0).
-#define LKF_SUB(k)                                                                    \
-    do {                                                                              \
-        if (L == 1 && a.trace && blockIdx.x == a.trace_block && threadIdx.x == 0)     \
-            a.trace[2 + 6 * nL + 1 + (k)] = __builtin_amdgcn_s_memrealtime();         \
+#define LKF_TRACE_MAX 256
+// Stage timestamps of the traced block (thread 0), kept in LDS and copied
+// out at the end so that tracing adds no global-memory traffic mid-stage;
+// LKF_SUB marks sub-steps of layer 1.
+#define LKF_MARK(k)                                                 \
+    do {                                                            \
+        if (tracing && threadIdx.x == 0) ltr[(k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
-#define LKF_MARK(k)                                                          \
-    do {                                                                     \
-        if (a.trace && blockIdx.x == a.trace_block && threadIdx.x == 0)      \
-            a.trace[(k)] = __builtin_amdgcn_s_memrealtime();                 \
+#define LKF_SUB(k)                                                  \
+    do {                                                            \
+        if (L == 1) LKF_MARK(2 + 6 * nL + 1 + (k));                 \
     } while (0)
 
 namespace lkf {
@@ -130,8 +130,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
-// math::rmsnorm (src/math.rs:45-49) of the LDS vector xr into xo.
-__device__ __forceinline__ void rmsnorm_lds(const float* xr, const float* __restrict__ g, uint32_t n, float eps,
+// math::rmsnorm (src/math.rs:45-49) of the LDS vector xr into xo (gains g in LDS).
+__device__ __forceinline__ void rmsnorm_lds(const float* xr, const float* g, uint32_t n, float eps,
                                             float* xo, float* red) {
     float ss = 0.f;
     for (uint32_t i = threadIdx.x; i < n; i += FT) ss = fmaf(xr[i], xr[i], ss);
@@ -161,8 +161,8 @@ __device__ __forceinline__ void kv8(const float* p, float* o) {
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-__device__ __forceinline__ void rot(float& x0, float& x1, float ang) {
-    const float s = sinf(ang), c = cosf(ang);
+// RoPE pair rotation (src/model.rs:268-279) by the angle with cosine c, sine s.
+__device__ __forceinline__ void rot(float& x0, float& x1, float c, float s) {
     const float n0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
     const float n1 = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
     x0 = n0;
@@ -212,7 +212,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     float* xin = lds;                 // vmax: the (normalised) input vector of a stage
     float* xres = xin + vmax;         // h: the residual stream of this layer
     float* red = xres + h;            // 16: block reductions
-    float* wv = red + 16;             // FW * 256: per wave q, this token's k and v, P
+    float* gin = red + 16;            // h: this layer's input_layernorm gains
+    float* gpost = gin + h;           // h: this layer's post_attention_layernorm gains
+    uint64_t* ltr = (uint64_t*)(gpost + h + (h & 1));  // LKF_TRACE_MAX stage timestamps
+    float* wv = (float*)(ltr + LKF_TRACE_MAX);  // FW * 256: per wave q, this token's k and v, P
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: stage branches stay scalar
     float* wq = wv + wave * 256;      // [64] the query head's q
@@ -245,13 +248,53 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         else if (hh < nh + nkv) { kind = 1; head = hh - nh; }
         else { kind = 2; head = hh - nh - nkv; }
     }
+    const bool tracing = a.trace && blockIdx.x == a.trace_block;
+    if (tracing && threadIdx.x == 0)
+        for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) ltr[k] = 0;
     Row<WT, NCHH> q1, q2;  // prefetched one stage ahead (layer L's rows during layer L-1's down)
-    if (has1) {
-        const LkFusedLayer& l0 = a.layers[0];
-        const LkDevW& w = kind == 0 ? l0.q : (kind == 1 ? l0.k : l0.v);
+    float b1 = 0.f, b2 = 0.f;  // their biases
+    auto issue_qkv = [&](const LkFusedLayer& l) {
+        const LkDevW& w = kind == 0 ? l.q : (kind == 1 ? l.k : l.v);
         row_issue(q1, w, head * 64 + ip, lane);
         row_issue(q2, w, head * 64 + ip + 32, lane);
+        const float* bias = kind == 0 ? l.bq : (kind == 1 ? l.bk : l.bv);
+        if (bias) {
+            b1 = bias[head * 64 + ip];
+            b2 = bias[head * 64 + ip + 32];
+        }
+    };
+    if (has1) issue_qkv(a.layers[0]);
+    // the same rotation angle every layer: pos * theta^(-2 ip / 64)
+    float rc = 1.f, rsn = 0.f;
+    if (has1 && kind < 2) {
+        const float ang = __fmul_rn(fpos, a.freq.f[ip]);
+        rsn = sinf(ang);
+        rc = cosf(ang);
     }
+    // a layer's RMSNorm gains go to LDS one layer ahead (loaded into
+    // registers during the previous layer's down stage)
+    constexpr int LKF_NPT = (NCHH * 64 * (int)ChunkTraits<WT>::elems + FT - 1) / FT;  // gains per thread
+    float ngi[LKF_NPT], ngp[LKF_NPT];
+    auto gains_issue = [&](const LkFusedLayer& l) {
+#pragma unroll
+        for (int k = 0; k < LKF_NPT; k++) {
+            const uint32_t i = threadIdx.x + k * FT;
+            ngi[k] = i < h ? l.in_norm[i] : 0.f;
+            ngp[k] = i < h ? l.post_norm[i] : 0.f;
+        }
+    };
+    auto gains_store = [&]() {
+#pragma unroll
+        for (int k = 0; k < LKF_NPT; k++) {
+            const uint32_t i = threadIdx.x + k * FT;
+            if (i < h) {
+                gin[i] = ngi[k];
+                gpost[i] = ngp[k];
+            }
+        }
+    };
+    gains_issue(a.layers[0]);
+    gains_store();
 
     LKF_MARK(0);
     // S0: every block takes the embedding row itself (src/model.rs:200-202).
@@ -268,30 +311,26 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         uint64_t* AB = a.ab + (size_t)par * qd;
         uint64_t* XP = a.xpb + (size_t)par * h;
         uint64_t* IB = a.ib + (size_t)par * I;
-        // Weight rows are issued right after a stage's input has arrived, one
-        // or two stages before they are used: vector loads retire in issue
-        // order, so a prefetch issued before a wait would delay that wait.
-        // (The attention stage needs most registers, so only the o_proj row
-        // is held across it.)
+        // Weight rows are issued one or two stages before they are used, after
+        // the stage's own outputs are published: vector loads retire in issue
+        // order (a prefetch issued before a wait delays that wait) and issuing
+        // stalls while the CU's memory queue is full.  (The attention stage
+        // needs most registers, so only the o_proj row is held across it.)
         const uint32_t U5 = I;              // gate/up rows
         Row<WT, NCHH> orow;                 // issued in S1, used in S4
         Row<WT, NCHH> gq[3], uq[3];         // issued in S4, used in S5
         Row<WT, NCHI> dn;                   // issued in S5, used in S6
         // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
         if (L > 0) stage_in(c, a.xb + (size_t)par * h, h, ep, xres);
-        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
-        rmsnorm_lds(xres, ly.in_norm, h, a.eps, xin, red);
+        rmsnorm_lds(xres, gin, h, a.eps, xin, red);
         if (has1) {
             float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
             float d2 = lk_wave_sum(row_dot(q2, xin, h, lane));
             if (lane == 0) {
                 const uint32_t r = head * 64 + ip;
-                const float* bias = kind == 0 ? ly.bq : (kind == 1 ? ly.bk : ly.bv);
-                if (bias) {
-                    d1 += bias[r];
-                    d2 += bias[r + 32];
-                }
-                if (kind < 2) rot(d1, d2, __fmul_rn(fpos, a.freq.f[ip]));
+                d1 += b1;  // zero when the model has no q/k/v biases
+                d2 += b2;
+                if (kind < 2) rot(d1, d2, rc, rsn);
                 if (kind == 0) {
                     publish(QB + r, d1, ep);
                     publish(QB + r + 32, d2, ep);
@@ -306,6 +345,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
             }
         }
+        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
         LKF_MARK(2 + 6 * L + 0);
         // ---------------- S2: attention partials.  Item = (query head, chunk of
         // TPW tiles of 64 positions), one wave each, spread over the grid: a
@@ -448,34 +488,30 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         if (c.gw < (int)nh) {
             const uint32_t hq = (uint32_t)c.gw;
             const uint64_t* pp = PB + (size_t)hq * nps * 66;
-            float M = -INFINITY, Ls = 0.f, A = 0.f;
-            for (uint32_t k0 = 0; k0 < nch; k0 += 4) {  // four chunks' loads in flight at once
-                uint64_t w[12];
+            // one round trip: lane k < nch fetches chunk k's (m, l); every lane
+            // fetches its dim of every chunk's acc
+            const bool mk = lane < (int)nch;
+            const uint64_t* pm = pp + (mk ? lane : 0) * 66;
+            const uint64_t wmw = mk ? ld_word(pm) : 0, wlw = mk ? ld_word(pm + 1) : 0;
+            uint64_t wa[LK_FUSED_PARTS];
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const bool ok = k0 + k < nch;
-                    const uint64_t* q0 = pp + (k0 + k) * 66;
-                    w[3 * k] = ok ? ld_word(q0) : 0;
-                    w[3 * k + 1] = ok ? ld_word(q0 + 1) : 0;
-                    w[3 * k + 2] = ok ? ld_word(q0 + 2 + lane) : 0;
-                }
+            for (int k = 0; k < (int)LK_FUSED_PARTS; k++) wa[k] = k < (int)nch ? ld_word(pp + k * 66 + 2 + lane) : 0;
+            float mv = -INFINITY, lv = 0.f;
+            if (mk) {
+                mv = (uint32_t)(wmw >> 32) == ep ? __uint_as_float((uint32_t)wmw) : await(c, pm, ep);
+                lv = (uint32_t)(wlw >> 32) == ep ? __uint_as_float((uint32_t)wlw) : await(c, pm + 1, ep);
+            }
+            const float M = lk_wave_max(mv);
+            const float sc = mk ? expf(mv - M) : 0.f;  // chunk k's weight, held by lane k
+            const float Ls = lk_wave_sum(sc * lv);
+            float A = 0.f;
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    if (k0 + k < nch) {
-                        const uint64_t* q0 = pp + (k0 + k) * 66;
-                        const uint64_t* src[3] = {q0, q0 + 1, q0 + 2 + lane};
-                        float v[3];
-#pragma unroll
-                        for (int i = 0; i < 3; i++)
-                            v[i] = (uint32_t)(w[3 * k + i] >> 32) == ep ? __uint_as_float((uint32_t)w[3 * k + i])
-                                                                        : await(c, src[i], ep);
-                        // (m, l, acc) folded online: rescale to the larger max
-                        const float Mn = fmaxf(M, v[0]);
-                        const float so = expf(M - Mn), sn = expf(v[0] - Mn);
-                        Ls = fmaf(Ls, so, sn * v[1]);
-                        A = fmaf(A, so, sn * v[2]);
-                        M = Mn;
-                    }
+            for (int k = 0; k < (int)LK_FUSED_PARTS; k++) {
+                if (k < (int)nch) {
+                    const float av = (uint32_t)(wa[k] >> 32) == ep ? __uint_as_float((uint32_t)wa[k])
+                                                                   : await(c, pp + k * 66 + 2 + lane, ep);
+                    const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), k));
+                    A = fmaf(sk, av, A);
                 }
             }
             publish(AB + hq * 64 + lane, A / Ls, ep);
@@ -485,6 +521,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         {
             const int u = c.gw;
             stage_in(c, AB, qd, ep, xin);
+            LKF_SUB(12);
+            if (u < (int)h) {
+                const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
+                if (lane == 0) publish(XP + u, xres[u] + d, ep);
+            }
+            LKF_SUB(13);
+            // the next stage's rows: issued after the publish, because issuing
+            // stalls once the CU's memory queue is full
 #pragma unroll
             for (int k = 0; k < 3; k++) {
                 const int uu = c.gw + k * c.nw;
@@ -493,23 +537,15 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     row_issue(uq[k], ly.up, (uint32_t)uu, lane);
                 }
             }
-            if (u < (int)h) {
-                const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
-                if (lane == 0) publish(XP + u, xres[u] + d, ep);
-            }
+            LKF_SUB(14);
         }
         LKF_MARK(2 + 6 * L + 3);
         // ---------------- S5: RMSNorm + gate/up + SwiGLU -> inner
         {
             stage_in(c, XP, h, ep, xres);
-            if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
-            if (has1 && L + 1 < nL) {  // the next layer's q/k/v rows
-                const LkFusedLayer& ln = a.layers[L + 1];
-                const LkDevW& w = kind == 0 ? ln.q : (kind == 1 ? ln.k : ln.v);
-                row_issue(q1, w, head * 64 + ip, lane);
-                row_issue(q2, w, head * 64 + ip + 32, lane);
-            }
-            rmsnorm_lds(xres, ly.post_norm, h, a.eps, xin, red);
+            LKF_SUB(8);
+            rmsnorm_lds(xres, gpost, h, a.eps, xin, red);
+            LKF_SUB(9);
 #pragma unroll
             for (int k = 0; k < 3; k++) {
                 const int uu = c.gw + k * c.nw;
@@ -519,6 +555,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
                 }
             }
+            LKF_SUB(10);
+            LKF_SUB(11);
             for (int uu = c.gw + 3 * c.nw; uu < (int)U5; uu += c.nw) {  // wider than 3 rows per wave
                 Row<WT, NCHH> gr, pr;
                 row_issue(gr, ly.gate, (uint32_t)uu, lane);
@@ -527,6 +565,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 const float up = lk_wave_sum(row_dot(pr, xin, h, lane));
                 if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
             }
+            if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
+            if (has1 && L + 1 < nL) issue_qkv(a.layers[L + 1]);  // the next layer's q/k/v rows
         }
         LKF_MARK(2 + 6 * L + 4);
         // ---------------- S6: down + residual -> x of layer L+1
@@ -544,6 +584,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 const float d = lk_wave_sum(row_dot(rr, xin, I, lane));
                 if (lane == 0) publish(XN + uu, xres[uu] + d, epn);
             }
+            if (L + 1 < nL) {  // read after the next stage_in's barrier
+                gains_issue(a.layers[L + 1]);
+                gains_store();
+            }
         }
         LKF_MARK(2 + 6 * L + 5);
     }
@@ -552,6 +596,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // (lmhead.hip); every block has read `base`, so the epoch may advance.
     LKF_MARK(2 + 6 * nL);
     if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch[0] = base + 1;
+    if (tracing && threadIdx.x == 0)
+        for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) a.trace[k] = ltr[k];
 }
 
 }  // namespace lkf
@@ -562,7 +608,7 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
     (void)max_chunks;
     uint32_t vmax = I > h ? I : h;
     if (nh * 64 > vmax) vmax = nh * 64;
-    return ((size_t)vmax + h + 16 + (size_t)FW * 256) * 4;
+    return ((size_t)vmax + h + 16 + 2 * (size_t)h + (h & 1) + 2 * LKF_TRACE_MAX + (size_t)FW * 256) * 4;
 }
 int lk_fused_threads() { return FT; }
 
