@@ -41,6 +41,8 @@
 #define FT (FW * 64)
 #define FCH 64
 #define LKF_TRACE_MAX 256
+#define LKF_KB 3  // gate/up units per wave of half 1, issued in S1
+#define LKF_KA 2  // gate/up units per wave of half 0, issued in S4
 // Stage timestamps of the traced block (thread 0), kept in LDS and copied
 // out at the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
@@ -113,9 +115,16 @@ __device__ __forceinline__ void await8(const Ctx& c, const uint64_t* src, uint32
 }
 
 // Block-cooperative: wait for n published words into LDS.
-__device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst) {
+// Block-cooperative: wait for n published words into LDS.  Only the waves of
+// one half (half 0: waves 0..FW/2-1, half 1: the rest) poll: a wave's loads
+// retire in issue order, so the polling half is the one with no weight rows
+// of its own still streaming in.
+__device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst,
+                                         int half) {
     __syncthreads();  // every wave is done reading dst from the previous stage
-    for (uint32_t i = threadIdx.x; i < n; i += 8 * FT) await8(c, src, i, FT, n, ep, dst);
+    const uint32_t t = threadIdx.x - (uint32_t)half * (FT / 2);
+    if ((int)(threadIdx.x >= FT / 2) == half)
+        for (uint32_t i = t; i < n; i += 8 * (FT / 2)) await8(c, src, i, FT / 2, n, ep, dst);
     __syncthreads();
 }
 
@@ -273,21 +282,22 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     }
     // a layer's RMSNorm gains go to LDS one layer ahead (loaded into
     // registers during the previous layer's down stage)
-    constexpr int LKF_NPT = (NCHH * 64 * (int)ChunkTraits<WT>::elems + FT - 1) / FT;  // gains per thread
+    // (loaded by half 0 only: half 1 polls first in the next layer)
+    constexpr int LKF_NPT = (NCHH * 64 * (int)ChunkTraits<WT>::elems + FT / 2 - 1) / (FT / 2);  // gains per thread
     float ngi[LKF_NPT], ngp[LKF_NPT];
     auto gains_issue = [&](const LkFusedLayer& l) {
 #pragma unroll
         for (int k = 0; k < LKF_NPT; k++) {
-            const uint32_t i = threadIdx.x + k * FT;
-            ngi[k] = i < h ? l.in_norm[i] : 0.f;
-            ngp[k] = i < h ? l.post_norm[i] : 0.f;
+            const uint32_t i = threadIdx.x + k * (FT / 2);
+            ngi[k] = (threadIdx.x < FT / 2 && i < h) ? l.in_norm[i] : 0.f;
+            ngp[k] = (threadIdx.x < FT / 2 && i < h) ? l.post_norm[i] : 0.f;
         }
     };
     auto gains_store = [&]() {
 #pragma unroll
         for (int k = 0; k < LKF_NPT; k++) {
-            const uint32_t i = threadIdx.x + k * FT;
-            if (i < h) {
+            const uint32_t i = threadIdx.x + k * (FT / 2);
+            if (threadIdx.x < FT / 2 && i < h) {
                 gin[i] = ngi[k];
                 gpost[i] = ngp[k];
             }
@@ -317,11 +327,20 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // stalls while the CU's memory queue is full.  (The attention stage
         // needs most registers, so only the o_proj row is held across it.)
         const uint32_t U5 = I;              // gate/up rows
+        // gate/up units: half 1 (waves FW/2..) holds LKF_KB units, issued in S1
+        // (it has no other work before S5); half 0 holds LKF_KA, issued in S4
+        // after its o_proj rows; the rest (wide models) are done in S5 directly.
+        const int nwh = c.nw / 2;
+        const bool half1 = wave >= FW / 2;
+        auto unit_of = [&](int k) -> int {
+            return half1 ? (c.gw - nwh) + k * nwh : LKF_KB * nwh + c.gw + k * nwh;
+        };
+        const int nunits = half1 ? LKF_KB : LKF_KA;
         Row<WT, NCHH> orow;                 // issued in S1, used in S4
-        Row<WT, NCHH> gq[3], uq[3];         // issued in S4, used in S5
+        Row<WT, NCHH> gq[LKF_KB], uq[LKF_KB];  // issued in S1 (half 1) or S4 (half 0), used in S5
         Row<WT, NCHI> dn;                   // issued in S5, used in S6
         // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
-        if (L > 0) stage_in(c, a.xb + (size_t)par * h, h, ep, xres);
+        if (L > 0) stage_in(c, a.xb + (size_t)par * h, h, ep, xres, 1);
         rmsnorm_lds(xres, gin, h, a.eps, xin, red);
         if (has1) {
             float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
@@ -346,6 +365,16 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
         }
         if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
+        if (half1) {
+#pragma unroll
+            for (int k = 0; k < LKF_KB; k++) {
+                const int uu = unit_of(k);
+                if (uu < (int)U5) {
+                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
+                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                }
+            }
+        }
         LKF_MARK(2 + 6 * L + 0);
         // ---------------- S2: attention partials.  Item = (query head, chunk of
         // TPW tiles of 64 positions), one wave each, spread over the grid: a
@@ -520,21 +549,23 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // ---------------- S4: o_proj + residual -> x'
         {
             const int u = c.gw;
-            stage_in(c, AB, qd, ep, xin);
+            stage_in(c, AB, qd, ep, xin, 0);
             LKF_SUB(12);
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
                 if (lane == 0) publish(XP + u, xres[u] + d, ep);
             }
             LKF_SUB(13);
-            // the next stage's rows: issued after the publish, because issuing
-            // stalls once the CU's memory queue is full
+            // the next stage's rows: issued after the publish, because a wave
+            // stalls at issue while its own earlier loads fill its queue
+            if (!half1) {
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                const int uu = c.gw + k * c.nw;
-                if (uu < (int)U5) {
-                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
-                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                for (int k = 0; k < LKF_KA; k++) {
+                    const int uu = unit_of(k);
+                    if (uu < (int)U5) {
+                        row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
+                        row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                    }
                 }
             }
             LKF_SUB(14);
@@ -542,14 +573,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         LKF_MARK(2 + 6 * L + 3);
         // ---------------- S5: RMSNorm + gate/up + SwiGLU -> inner
         {
-            stage_in(c, XP, h, ep, xres);
+            stage_in(c, XP, h, ep, xres, 1);
             LKF_SUB(8);
             rmsnorm_lds(xres, gpost, h, a.eps, xin, red);
             LKF_SUB(9);
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                const int uu = c.gw + k * c.nw;
-                if (uu < (int)U5) {
+            for (int k = 0; k < LKF_KB; k++) {
+                const int uu = unit_of(k);
+                if (k < nunits && uu < (int)U5) {
                     const float gg = lk_wave_sum(row_dot(gq[k], xin, h, lane));
                     const float up = lk_wave_sum(row_dot(uq[k], xin, h, lane));
                     if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
@@ -557,7 +588,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
             LKF_SUB(10);
             LKF_SUB(11);
-            for (int uu = c.gw + 3 * c.nw; uu < (int)U5; uu += c.nw) {  // wider than 3 rows per wave
+            for (int uu = (LKF_KA + LKF_KB) * nwh + c.gw; uu < (int)U5; uu += c.nw) {  // wider models
                 Row<WT, NCHH> gr, pr;
                 row_issue(gr, ly.gate, (uint32_t)uu, lane);
                 row_issue(pr, ly.up, (uint32_t)uu, lane);
@@ -573,7 +604,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         {
             const uint32_t epn = ep + 1;
             uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * h;
-            stage_in(c, IB, I, ep, xin);
+            stage_in(c, IB, I, ep, xin, 1);
             if (c.gw < (int)h) {
                 const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
                 if (lane == 0) publish(XN + c.gw, xres[c.gw] + d, epn);
