@@ -76,7 +76,7 @@ def cpu_baseline(cfg, tensors, prompt_len: int, budget_s: float) -> dict:
     om = oracle.Model(cfg, tensors)
     rng = np.random.default_rng(11)
     prompt = rng.integers(0, cfg.vocab_size, prompt_len).astype(np.uint32)
-    n_max = 64
+    n_max = 4096
     s = om.session(prompt_len + n_max + 2)
     lo = s.prefill(prompt)  # untimed, as generate.rs times decode only
     cur = oracle.argmax(lo)
@@ -107,8 +107,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=32)
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--cpu-prompt", type=int, default=16)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-prompt", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
