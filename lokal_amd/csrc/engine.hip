@@ -328,8 +328,8 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "wider or deeper than the one-kernel step takes";
         return LKHIP_OK;
     }
-    if (c.num_attention_heads * LK_FUSED_PARTS > nw) {
-        e->fused_why = "more attention items than waves";
+    if (c.num_attention_heads * ((LK_FUSED_MAX_SEQ + 63) / 64) > nw) {
+        e->fused_why = "more attention tiles than waves";
         return LKHIP_OK;
     }
     // LDS limit for the longest session the one-kernel step serves
@@ -471,7 +471,8 @@ struct lkhip_session {
     lkhip_engine* e = nullptr;
     size_t max_seq = 0;
     hipStream_t stream = nullptr;
-    DevBuf kc, vc;  // [layer][n_kv][max_seq][64], f16 or f32 (kv_f32)
+    DevBuf kc, vc;  // [layer][n_kv][kv_seq][64], f16 or f32 (kv_f32)
+    size_t kv_seq = 0;  // cache rows per kv head: max_seq rounded up to whole 64-position tiles
     int kv_f32 = 0;
     DevBuf x, xn, qkv, att, inner, logits, part, keys, head_epoch, err, state, feed, ids_out;
     LkStepState* h_state = nullptr;  // pinned
@@ -503,7 +504,7 @@ struct lkhip_session {
 };
 
 static size_t kv_layer_elems(const lkhip_session* s) {
-    return (size_t)s->e->cfg.num_key_value_heads * s->max_seq * 64;
+    return (size_t)s->e->cfg.num_key_value_heads * s->kv_seq * 64;
 }
 
 // Records one launch for profiling: an event after every launch.
@@ -583,7 +584,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.kc = s->kc.p;
         a.vc = s->vc.p;
         a.kv_layer = kv_layer_elems(s);
-        a.max_seq = (uint32_t)s->max_seq;
+        a.max_seq = (uint32_t)s->kv_seq;
         a.max_chunks = s->max_chunks;
         a.st = state;
         a.epoch = s->epoch.as<uint32_t>();
@@ -625,7 +626,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         uint8_t* vc = s->vc.as<uint8_t>() + (size_t)L * kv_layer_elems(s) * kv_el;
         STEP(lk_rope_kv_launch(qkv, c.num_attention_heads, c.num_key_value_heads, e->freq, state, nullptr, 1, kc, vc,
                                s->kv_f32,
-                               (uint32_t)s->max_seq, 0, nullptr, st),
+                               (uint32_t)s->kv_seq, 0, nullptr, st),
              C_OTHER, 0);
         {
             LkAttnArgs a{};
@@ -639,7 +640,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             a.n_seq = 1;
             a.n_heads = c.num_attention_heads;
             a.n_kv = c.num_key_value_heads;
-            a.max_seq = (uint32_t)s->max_seq;
+            a.max_seq = (uint32_t)s->kv_seq;
             a.seq_stride = 0;
             a.q_stride = e->qd;
             STEP(lk_attn_launch(a, st), C_ATTN, 0);
@@ -703,6 +704,7 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
     auto s = std::make_unique<lkhip_session>();
     s->e = e;
     s->max_seq = max_seq;
+    s->kv_seq = (max_seq + 63) / 64 * 64;
     const lkhip_config& c = e->cfg;
     HIP_OR_FAIL(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     int rc;
@@ -714,7 +716,7 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         (rc = dev_alloc(s->inner, (size_t)c.intermediate_size * 4)) ||
         (rc = dev_alloc(s->logits, (size_t)c.vocab_size * 4)))
         return rc;
-    if ((rc = dev_alloc(s->part, lk_attn_part_floats(1, c.num_attention_heads, (uint32_t)max_seq) * 4))) return rc;
+    if ((rc = dev_alloc(s->part, lk_attn_part_floats(1, c.num_attention_heads, (uint32_t)s->kv_seq) * 4))) return rc;
     s->head_blocks = lk_lm_head_blocks(c.vocab_size, e->lm_head->dw.type, c.hidden_size);
     if ((rc = dev_alloc(s->keys, (size_t)LK_HEAD_MAX_BLOCKS * 2 * 8)) || (rc = dev_alloc(s->head_epoch, 4)) ||
         (rc = dev_alloc(s->err, 4)))
@@ -726,7 +728,7 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         const size_t qkvd = e->qd + 2 * e->kvd;
         s->max_chunks = (uint32_t)((max_seq + 63) / 64);
         if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
-            (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * std::min(s->max_chunks, LK_FUSED_PARTS) * 66 * 8)) ||
+            (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * s->max_chunks * 66 * 8)) ||
             (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
             (rc = dev_alloc(s->ib, 2 * I * 8)) ||
             (rc = dev_alloc(s->epoch, 4)))
@@ -913,7 +915,7 @@ extern "C" int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t po
     const uint8_t* base = (which_v ? s->vc : s->kc).as<uint8_t>() + (size_t)layer * kv_layer_elems(s) * el;
     std::vector<uint8_t> h(64 * el);
     for (uint32_t kh = 0; kh < c.num_key_value_heads; kh++) {
-        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->max_seq + pos) * 64 * el, 64 * el,
+        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->kv_seq + pos) * 64 * el, 64 * el,
                               hipMemcpyDeviceToHost));
         if (s->kv_f32) {
             memcpy(&out[kh * 64], h.data(), 256);

@@ -30,7 +30,7 @@ struct LkFusedArgs {
     // exchange buffers of (f32 | epoch) words, two copies by layer parity
     uint64_t* xb;   // [2][h]        layer input x
     uint64_t* qb;   // [2][qd+2kvd]  rotated q, this token's k and v
-    uint64_t* pb;   // [2][nh][min(max_chunks, LK_FUSED_PARTS)][66] attention partials (m, l, acc[64])
+    uint64_t* pb;   // [2][nh][max_chunks][66] attention partials of each 64-position tile (m, l, acc[64])
     uint64_t* ab;   // [2][qd]       attention output
     uint64_t* xpb;  // [2][h]        x after the attention residual
     uint64_t* ib;   // [2][I]        SwiGLU output
@@ -55,9 +55,7 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_MAX_SEQ 4096u
 // Waves per workgroup.
 #define LK_FUSED_WAVES 8u
-// Attention partials per query head: a head's tiles are split into at most
-// this many chunks, one wave each.
-#define LK_FUSED_PARTS 16u
+
 int lk_fused_threads();
 // setup=true checks the shape is instantiated, sets the LDS limit and checks
 // one block fits per CU; setup=false launches `blocks` blocks.

@@ -115,16 +115,20 @@ __device__ __forceinline__ void await8(const Ctx& c, const uint64_t* src, uint32
 }
 
 // Block-cooperative: wait for n published words into LDS.
-// Block-cooperative: wait for n published words into LDS.  Only the waves of
-// one half (half 0: waves 0..FW/2-1, half 1: the rest) poll: a wave's loads
-// retire in issue order, so the polling half is the one with no weight rows
-// of its own still streaming in.
+// Block-cooperative: wait for n published words into LDS.  half < 0: every
+// wave polls; otherwise only the waves of one half (half 0: waves 0..FW/2-1,
+// half 1: the rest) do: a wave's loads retire in issue order, so the polling
+// half is the one with no weight rows of its own still streaming in.
 __device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst,
                                          int half) {
     __syncthreads();  // every wave is done reading dst from the previous stage
-    const uint32_t t = threadIdx.x - (uint32_t)half * (FT / 2);
-    if ((int)(threadIdx.x >= FT / 2) == half)
-        for (uint32_t i = t; i < n; i += 8 * (FT / 2)) await8(c, src, i, FT / 2, n, ep, dst);
+    if (half < 0) {
+        for (uint32_t i = threadIdx.x; i < n; i += 8 * FT) await8(c, src, i, FT, n, ep, dst);
+    } else {
+        const uint32_t t = threadIdx.x - (uint32_t)half * (FT / 2);
+        if ((int)(threadIdx.x >= FT / 2) == half)
+            for (uint32_t i = t; i < n; i += 8 * (FT / 2)) await8(c, src, i, FT / 2, n, ep, dst);
+    }
     __syncthreads();
 }
 
@@ -241,10 +245,9 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     const uint32_t nL = a.n_layers;
     const float fpos = (float)pos;
     const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
-    // attention items: (query head, chunk of TPW consecutive tiles), one wave each
-    const uint32_t TPW = (ntile + LK_FUSED_PARTS - 1) / LK_FUSED_PARTS;
-    const uint32_t nch = (ntile + TPW - 1) / TPW;   // chunks per head, <= LK_FUSED_PARTS and <= max_chunks
-    const uint32_t nps = a.max_chunks < LK_FUSED_PARTS ? a.max_chunks : LK_FUSED_PARTS;  // partial slots per head
+    // attention items: (query head, 64-position tile), one wave each
+    const uint32_t nch = ntile;          // partials per head
+    const uint32_t nps = a.max_chunks;   // partial slots per head
 
     // S1 work of this wave: q/k/v rows (i, i+32) of one head
     const uint32_t U1 = (nh + 2 * nkv) * 32;
@@ -376,44 +379,44 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
         }
         LKF_MARK(2 + 6 * L + 0);
-        // ---------------- S2: attention partials.  Item = (query head, chunk of
-        // TPW tiles of 64 positions), one wave each, spread over the grid: a
-        // wave scores 64 positions at a time (lane = position), keeps an
-        // online softmax over its tiles and accumulates P.V with lane =
-        // (position group lane & 7, dims 8 * (lane >> 3) ..+7).
+        // ---------------- S2: attention partials.  Item = (query head, tile of
+        // 64 positions), one wave each, spread over the grid (items past the
+        // first half's waves, at long contexts, go to the second half): the
+        // wave scores its 64 positions (lane = position), takes the tile's
+        // softmax max and sum, and accumulates P.V with lane = (position
+        // group lane & 7, dims 8 * (lane >> 3) ..+7).
         if (c.gw < (int)(nh * nch)) {
             const uint32_t hq = (uint32_t)c.gw / nch, ck = (uint32_t)c.gw % nch;
             const uint32_t j = hq / G;
-            const uint32_t t0 = ck * TPW, t1 = (t0 + TPW < ntile) ? t0 + TPW : ntile;
-            const bool has_cur = t1 == ntile;  // the chunk holding position pos
+            const uint32_t t = ck;
+            const bool has_cur = t + 1 == ntile;  // the tile holding position pos
             LKF_SUB(0);
             const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
             const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
-            const uint32_t plast = pos > 0 ? pos - 1 : 0;
             const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
-            // cached positions (< pos) do not depend on this token.  Straight-line
-            // loads: positions >= pos read a clamped (valid) row, replaced or masked below.
+            // Cached positions (< pos) do not depend on this token: load them
+            // first.  The cache holds whole 64-position tiles (its per-head
+            // stride is max_seq rounded up to 64), so every row of the tile is
+            // in bounds; rows >= pos are replaced (pos) or masked (> pos) below.
+            // One base address per lane, the rest immediate offsets.
             uint4 kraw[KC], vraw[KC];
-            auto load_k = [&](uint32_t t) {
-                const uint32_t p = t * 64 + (uint32_t)lane;
-                const uint32_t pk = p < pos ? p : plast;
+            const KV* Kl = K + (t * 64u + (uint32_t)lane) * 64u;
+            const KV* Vl = V + (t * 64u + sub) * 64u + dq;
+            auto load_k = [&](uint32_t) {
 #pragma unroll
-                for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)(K + pk * 64u) + 16 * q);
+                for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
             };
-            auto load_v = [&](uint32_t t) {
+            auto load_v = [&](uint32_t) {
 #pragma unroll
-                for (int q = 0; q < KC; q++) {
-                    const uint32_t pj = t * 64 + (uint32_t)(KV32 ? q / 2 : q) * 8 + sub;
-                    const uint32_t dd = dq + (KV32 ? (q & 1) * 4 : 0);
-                    vraw[q] = *(const uint4*)(V + ((pj < pos ? pj : plast) * 64u + dd));
-                }
+                for (int q = 0; q < KC; q++)
+                    vraw[q] = *(const uint4*)(Vl + (KV32 ? (q / 2) * 8 * 64 + (q & 1) * 4 : q * 8 * 64));
             };
             // f16: a tile's K and V fit in registers together; f32: V follows the scores
             auto load_tile = [&](uint32_t t) {
                 load_k(t);
                 if constexpr (!KV32) load_v(t);
             };
-            load_tile(t0);
+            load_tile(t);
             LKF_SUB(1);
             {  // this head's q; this token's k and v for the chunk that holds pos
                 const uint64_t* sq = QB + hq * 64 + lane;
@@ -430,11 +433,11 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
             wave_sync_lds();
             LKF_SUB(2);
-            float m = -INFINITY, l = 0.f, acc[8];
+            float acc[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[e] = 0.f;
-            for (uint32_t t = t0; t < t1; t++) {
-                if (t > t0) load_tile(t);
+            float m, l;
+            {
                 const uint32_t p = t * 64 + (uint32_t)lane;
                 const bool valid = p <= pos;
                 if (p == pos) {  // this token's k packed like a cache row: one code path below
@@ -455,16 +458,12 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
                 LKF_SUB(3);
                 if constexpr (KV32) load_v(t);
-                // online softmax over the chunk's tiles (the split-invariant form
-                // of math::softmax, src/math.rs:55-66)
+                // the tile's part of math::softmax (src/math.rs:55-66); tiles
+                // are combined in S3 with the split-invariant rescaling
                 const float sg = valid ? s * 0.125f : -INFINITY;
-                const float mn = fmaxf(m, lk_wave_max(sg));
-                const float pe = valid ? expf(sg - mn) : 0.f;
-                const float rs = expf(m - mn);  // 0 on the first tile
-                l = fmaf(l, rs, lk_wave_sum(pe));
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[e] *= rs;
-                m = mn;
+                m = lk_wave_max(sg);
+                const float pe = valid ? expf(sg - m) : 0.f;
+                l = lk_wave_sum(pe);
                 wP[(lane & 7) * 8 + (lane >> 3)] = pe;  // [group][jj]: a lane's 8 weights are adjacent
                 wave_sync_lds();
                 LKF_SUB(4);
@@ -487,7 +486,6 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                         for (int e = 0; e < 8; e++) acc[e] = fmaf(pw, v8[e], acc[e]);
                     }
                 }
-                wave_sync_lds();  // wP is rewritten by the next tile
             }
             LKF_SUB(5);
             // Sum the 8 position groups of each dims chunk (8 adjacent lanes):
@@ -517,30 +515,53 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         if (c.gw < (int)nh) {
             const uint32_t hq = (uint32_t)c.gw;
             const uint64_t* pp = PB + (size_t)hq * nps * 66;
-            // one round trip: lane k < nch fetches chunk k's (m, l); every lane
-            // fetches its dim of every chunk's acc
+            // lane k < nch fetches tile k's (m, l); every lane fetches its dim
+            // of every tile's acc, 16 tiles' words in flight at a time, and
+            // every round re-polls all the words still missing together
             const bool mk = lane < (int)nch;
             const uint64_t* pm = pp + (mk ? lane : 0) * 66;
-            const uint64_t wmw = mk ? ld_word(pm) : 0, wlw = mk ? ld_word(pm + 1) : 0;
-            uint64_t wa[LK_FUSED_PARTS];
+            const uint64_t epw = (uint64_t)ep << 32;
+            uint64_t wmw = mk ? ld_word(pm) : epw, wlw = mk ? ld_word(pm + 1) : epw;
+            float mv = -INFINITY, lv = 0.f, M = 0.f, sc = 0.f, Ls = 0.f, A = 0.f;
+            for (uint32_t k0 = 0; k0 < nch; k0 += 16) {
+                uint64_t wa[16];
 #pragma unroll
-            for (int k = 0; k < (int)LK_FUSED_PARTS; k++) wa[k] = k < (int)nch ? ld_word(pp + k * 66 + 2 + lane) : 0;
-            float mv = -INFINITY, lv = 0.f;
-            if (mk) {
-                mv = (uint32_t)(wmw >> 32) == ep ? __uint_as_float((uint32_t)wmw) : await(c, pm, ep);
-                lv = (uint32_t)(wlw >> 32) == ep ? __uint_as_float((uint32_t)wlw) : await(c, pm + 1, ep);
-            }
-            const float M = lk_wave_max(mv);
-            const float sc = mk ? expf(mv - M) : 0.f;  // chunk k's weight, held by lane k
-            const float Ls = lk_wave_sum(sc * lv);
-            float A = 0.f;
+                for (int k = 0; k < 16; k++) wa[k] = k0 + k < nch ? ld_word(pp + (k0 + k) * 66 + 2 + lane) : epw;
+                for (uint32_t r = 0;; r++) {
+                    bool done = (uint32_t)(wmw >> 32) == ep && (uint32_t)(wlw >> 32) == ep;
 #pragma unroll
-            for (int k = 0; k < (int)LK_FUSED_PARTS; k++) {
-                if (k < (int)nch) {
-                    const float av = (uint32_t)(wa[k] >> 32) == ep ? __uint_as_float((uint32_t)wa[k])
-                                                                   : await(c, pp + k * 66 + 2 + lane, ep);
-                    const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), k));
-                    A = fmaf(sk, av, A);
+                    for (int k = 0; k < 16; k++) done &= (uint32_t)(wa[k] >> 32) == ep;
+                    if (done) break;
+                    if ((r & 255) == 255) {
+                        if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+                        if (r > (1u << 21)) {
+                            __hip_atomic_store(c.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            break;
+                        }
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    if ((uint32_t)(wmw >> 32) != ep) wmw = ld_word(pm);
+                    if ((uint32_t)(wlw >> 32) != ep) wlw = ld_word(pm + 1);
+#pragma unroll
+                    for (int k = 0; k < 16; k++)
+                        if ((uint32_t)(wa[k] >> 32) != ep) wa[k] = ld_word(pp + (k0 + k) * 66 + 2 + lane);
+                }
+                if (k0 == 0) {
+                    if (mk) {
+                        mv = __uint_as_float((uint32_t)wmw);
+                        lv = __uint_as_float((uint32_t)wlw);
+                    }
+                    M = lk_wave_max(mv);
+                    sc = mk ? expf(mv - M) : 0.f;  // tile k's weight, held by lane k
+                    Ls = lk_wave_sum(sc * lv);
+                }
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    if (k0 + k < nch) {
+                        const float sk = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), k0 + k));
+                        A = fmaf(sk, __uint_as_float((uint32_t)wa[k]), A);
+                    }
                 }
             }
             publish(AB + hq * 64 + lane, A / Ls, ep);
@@ -549,7 +570,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // ---------------- S4: o_proj + residual -> x'
         {
             const int u = c.gw;
-            stage_in(c, AB, qd, ep, xin, 0);
+            stage_in(c, AB, qd, ep, xin, -1);
             LKF_SUB(12);
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
