@@ -97,18 +97,19 @@ __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Words src[i0 + k*step], k < 8, i < n, into dst[...]: all eight loads are in
+// Words src[i0 + k*step], k < N, i < n, into dst[...]: all N loads are in
 // flight together; only words not yet carrying the epoch are polled again.
-__device__ __forceinline__ void await8(const Ctx& c, const uint64_t* src, uint32_t i0, uint32_t step, uint32_t n,
+template <int N>
+__device__ __forceinline__ void awaitN(const Ctx& c, const uint64_t* src, uint32_t i0, uint32_t step, uint32_t n,
                                        uint32_t ep, float* dst) {
-    uint64_t w[8];
+    uint64_t w[N];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < N; k++) {
         const uint32_t i = i0 + k * step;
         w[k] = i < n ? ld_word(src + i) : 0;
     }
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < N; k++) {
         const uint32_t i = i0 + k * step;
         if (i < n) dst[i] = (uint32_t)(w[k] >> 32) == ep ? __uint_as_float((uint32_t)w[k]) : await(c, src + i, ep);
     }
@@ -119,15 +120,17 @@ __device__ __forceinline__ void await8(const Ctx& c, const uint64_t* src, uint32
 // wave polls; otherwise only the waves of one half (half 0: waves 0..FW/2-1,
 // half 1: the rest) do: a wave's loads retire in issue order, so the polling
 // half is the one with no weight rows of its own still streaming in.
+// N: words in flight per thread (sized so one batch covers the vector).
+template <int N>
 __device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst,
                                          int half) {
     __syncthreads();  // every wave is done reading dst from the previous stage
     if (half < 0) {
-        for (uint32_t i = threadIdx.x; i < n; i += 8 * FT) await8(c, src, i, FT, n, ep, dst);
+        for (uint32_t i = threadIdx.x; i < n; i += N * FT) awaitN<N>(c, src, i, FT, n, ep, dst);
     } else {
         const uint32_t t = threadIdx.x - (uint32_t)half * (FT / 2);
         if ((int)(threadIdx.x >= FT / 2) == half)
-            for (uint32_t i = t; i < n; i += 8 * (FT / 2)) await8(c, src, i, FT / 2, n, ep, dst);
+            for (uint32_t i = t; i < n; i += N * (FT / 2)) awaitN<N>(c, src, i, FT / 2, n, ep, dst);
     }
     __syncthreads();
 }
@@ -343,7 +346,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         Row<WT, NCHH> gq[LKF_KB], uq[LKF_KB];  // issued in S1 (half 1) or S4 (half 0), used in S5
         Row<WT, NCHI> dn;                   // issued in S5, used in S6
         // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
-        if (L > 0) stage_in(c, a.xb + (size_t)par * h, h, ep, xres, 1);
+        if (L > 0) stage_in<8>(c, a.xb + (size_t)par * h, h, ep, xres, 1);
         rmsnorm_lds(xres, gin, h, a.eps, xin, red);
         if (has1) {
             float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
@@ -570,7 +573,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // ---------------- S4: o_proj + residual -> x'
         {
             const int u = c.gw;
-            stage_in(c, AB, qd, ep, xin, -1);
+            stage_in<4>(c, AB, qd, ep, xin, -1);
             LKF_SUB(12);
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
@@ -594,7 +597,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         LKF_MARK(2 + 6 * L + 3);
         // ---------------- S5: RMSNorm + gate/up + SwiGLU -> inner
         {
-            stage_in(c, XP, h, ep, xres, 1);
+            stage_in<8>(c, XP, h, ep, xres, 1);
             LKF_SUB(8);
             rmsnorm_lds(xres, gpost, h, a.eps, xin, red);
             LKF_SUB(9);
@@ -625,7 +628,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         {
             const uint32_t epn = ep + 1;
             uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * h;
-            stage_in(c, IB, I, ep, xin, 1);
+            stage_in<24>(c, IB, I, ep, xin, 1);
             if (c.gw < (int)h) {
                 const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
                 if (lane == 0) publish(XN + c.gw, xres[c.gw] + d, epn);
