@@ -8,9 +8,11 @@
 //   scores : lane = position, the K row (128 B) is converted once and dotted
 //            against all G query rows (LDS broadcast reads);
 //   softmax: per-tile max / exp / sum by wave reductions;
-//   P.V    : lane = (position j%8 group, 8 dims), one 16-byte V load per lane
-//            covers 8 positions x 64 dims per instruction; the 8 lanes that share
-//            a dim slice are combined by xor-shuffles.
+//   P.V    : lane = (position group lane & 7, 8 dims), one 16-byte V load per
+//            lane covers 8 positions x 64 dims per instruction; the 8 lanes that
+//            share a dim slice are combined by DPP.
+// Loads are straight-line (positions past ctx re-read the last live row and
+// are masked), issued before the dependent arithmetic.
 // The 4 tiles merge in LDS into one (m, l, acc[64]) partial per query head;
 // attn_merge_kernel folds the partials of all chunks with the usual
 // max-rescaled sums.  fp32 throughout; scale 1/sqrt(64) = 0.125 is exact.
@@ -59,21 +61,34 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
     const KV* __restrict__ K = (const KV*)a.k + kv_base;
     const KV* __restrict__ V = (const KV*)a.v + kv_base;
+    constexpr bool KV32 = sizeof(KV) == 4;
 
     __shared__ float qs[G][LK_HD];
-    __shared__ float ps[4][G][64];
+    __shared__ float ps[4][G][64];      // [wave][head][group * 8 + jj]
     __shared__ float red_m[4][G], red_l[4][G];
     __shared__ float red_acc[4][G][LK_HD];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t p0 = c0 + (uint32_t)w * 64;
+    const bool tile_live = p0 < ctx;  // wave-uniform
+    const uint32_t plast = ctx - 1;
+    // Straight-line loads: positions past ctx re-read the last live row (in
+    // bounds) and are masked below.  K: lane = position, its whole 64-dim row.
+    const uint32_t p = p0 + (uint32_t)lane;
+    const KV* krow = K + (size_t)(p < ctx ? p : plast) * LK_HD;
+    float kf[LK_HD];
+    if (tile_live) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) load8(krow + 8 * i, kf + 8 * i);
+    }
     const float* qsrc = a.q + (size_t)seq * a.q_stride + (size_t)kvh * G * LK_HD;
     for (int i = tid; i < G * LK_HD; i += 256) qs[i / LK_HD][i % LK_HD] = qsrc[i];
     __syncthreads();
 
-    const uint32_t p0 = c0 + (uint32_t)w * 64;
-    const bool tile_live = p0 < ctx;
-    float m[G], l[G];
-    float acc[G][8];
+    // P.V lane map: position group sub = lane & 7, dims dq..dq+7 (dq = 8 * (lane >> 3))
+    const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
+    float m[G], l[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         m[g] = -INFINITY;
@@ -81,25 +96,30 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
     }
-
     if (tile_live) {
-        // ---- scores: lane = position
-        const uint32_t p = p0 + (uint32_t)lane;
+        // V for the P.V pass, issued before the scores so it is in flight meanwhile
+        float vf[8][8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const uint32_t pj = p0 + (uint32_t)jj * 8 + sub;
+            load8(V + (size_t)(pj < ctx ? pj : plast) * LK_HD + dq, vf[jj]);
+        }
+        // ---- scores: lane = position, q rows by LDS broadcast
         const bool valid = p < ctx;
         float s[G];
 #pragma unroll
         for (int g = 0; g < G; g++) s[g] = 0.f;
-        if (valid) {
-            const KV* krow = K + (size_t)p * LK_HD;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float k8[8];
-                load8(krow + 8 * i, k8);
+        for (int i = 0; i < 16; i++) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-#pragma unroll
-                    for (int g = 0; g < G; g++) s[g] = fmaf(k8[e], qs[g][8 * i + e], s[g]);
-                }
+            for (int g = 0; g < G; g++) {
+                const float4 qv = *(const float4*)&qs[g][4 * i];
+                float t = s[g];
+                t = fmaf(kf[4 * i], qv.x, t);
+                t = fmaf(kf[4 * i + 1], qv.y, t);
+                t = fmaf(kf[4 * i + 2], qv.z, t);
+                t = fmaf(kf[4 * i + 3], qv.w, t);
+                s[g] = t;
             }
         }
 #pragma unroll
@@ -108,36 +128,30 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
             m[g] = lk_wave_max(sg);
             const float pg = valid ? expf(sg - m[g]) : 0.f;
             l[g] = lk_wave_sum(pg);
-            ps[w][g][lane] = pg;
+            ps[w][g][(lane & 7) * 8 + (lane >> 3)] = pg;  // position lane -> [group][jj]
         }
-    }
-    __syncthreads();  // P of every tile is in LDS
-
-    if (tile_live) {
-        // ---- P.V: lane = (position group, 8-dim slice)
-        const uint32_t sub = (uint32_t)lane >> 3, dq = ((uint32_t)lane & 7) * 8;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's P is in LDS
+        __builtin_amdgcn_wave_barrier();
+        // ---- P.V (weights of masked positions are 0 and their V rows are finite)
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t pj = p0 + (uint32_t)j * 8 + sub;
-            if (pj < ctx) {
-                float vf[8];
-                load8(V + (size_t)pj * LK_HD + dq, vf);
+        for (int jj = 0; jj < 8; jj++) {
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float pw = ps[w][g][j * 8 + sub];
+            for (int g = 0; g < G; g++) {
+                const float pw = ps[w][g][sub * 8 + jj];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pw, vf[e], acc[g][e]);
-                }
+                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pw, vf[jj][e], acc[g][e]);
             }
         }
+        // sum the 8 position groups of each dims chunk (8 adjacent lanes) by
+        // DPP: quad pairs, quad halves, row_ror 4 -> lanes 4..7 of each 8 hold it
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 float v = acc[g][e];
-                v += __shfl_xor(v, 8, 64);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
+                v += lk_dpp<0xB1, 0xF>(v, 0.f);
+                v += lk_dpp<0x4E, 0xF>(v, 0.f);
+                v += lk_dpp<0x124, 0xF>(v, 0.f);
                 acc[g][e] = v;
             }
     }
@@ -148,11 +162,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
             red_l[w][g] = l[g];
         }
     }
-    if (lane < 8) {
+    if ((lane & 7) == 4) {
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) red_acc[w][g][lane * 8 + e] = acc[g][e];
+            for (int e = 0; e < 8; e++) red_acc[w][g][dq + e] = acc[g][e];
     }
     __syncthreads();
 
@@ -181,23 +195,66 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     }
 }
 
-// Fold the chunk partials of one query head: out = sum_c e^{m_c-M} acc_c / sum_c e^{m_c-M} l_c.
-__global__ __launch_bounds__(64) void attn_merge_kernel(const LkAttnArgs a) {
-    const uint32_t h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+// Fold the chunk partials of one query head: out = sum_c e^{m_c-M} acc_c /
+// sum_c e^{m_c-M} l_c.  Four waves take interleaved quarters of the chunks
+// (lane = dim; 16 chunks' words in flight per lane), each folding online
+// against its own running max, and combine their (m, l, acc) in LDS.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const LkAttnArgs a) {
+    const uint32_t h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t ctx = attn_ctx(a, seq);
     const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     const uint32_t nch = (ctx + LK_ACHUNK - 1) / LK_ACHUNK;
     const float* part = a.part + ((size_t)seq * a.n_heads + h) * max_chunks * (2 + LK_HD);
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; c++) M = fmaxf(M, part[(size_t)c * (2 + LK_HD)]);
-    float L = 0.f, A = 0.f;
-    for (uint32_t c = 0; c < nch; c++) {
-        const float* pc = part + (size_t)c * (2 + LK_HD);
-        const float sc = expf(pc[0] - M);
-        L = fmaf(sc, pc[1], L);
-        A = fmaf(sc, pc[2 + d], A);
+    __shared__ float wm[4], wl[4], wa[4][LK_HD];
+    float M = -INFINITY, L = 0.f, A = 0.f;
+    for (uint32_t c0 = w * 16; c0 < nch; c0 += 64) {  // this wave's next 16 chunks
+        float mv[16], lv[16], av[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const uint32_t c = c0 + k < nch ? c0 + k : c0;  // in-range reload, dropped below
+            const float* pc = part + (size_t)c * (2 + LK_HD);
+            mv[k] = pc[0];
+            lv[k] = pc[1];
+            av[k] = pc[2 + lane];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (c0 + k < nch) Mn = fmaxf(Mn, mv[k]);
+        const float rs = expf(M - Mn);  // 0 while M is still -inf
+        L *= rs;
+        A *= rs;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (c0 + k < nch) {
+                const float sc = expf(mv[k] - Mn);
+                L = fmaf(sc, lv[k], L);
+                A = fmaf(sc, av[k], A);
+            }
+        }
+        M = Mn;
     }
-    a.out[((size_t)seq * a.n_heads + h) * LK_HD + d] = A / L;
+    if (lane == 0) {
+        wm[w] = M;
+        wl[w] = L;
+    }
+    wa[w][lane] = A;
+    __syncthreads();
+    if (w != 0) return;
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; i++) Mt = fmaxf(Mt, wm[i]);
+    float Lt = 0.f, At = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (wm[i] != -INFINITY) {  // a wave with no chunks holds nothing
+            const float sc = expf(wm[i] - Mt);
+            Lt = fmaf(sc, wl[i], Lt);
+            At = fmaf(sc, wa[i][lane], At);
+        }
+    }
+    a.out[((size_t)seq * a.n_heads + h) * LK_HD + lane] = At / Lt;
 }
 
 hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
@@ -224,6 +281,6 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
 #undef LK_ATTN_CASE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.n_seq), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.n_seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }

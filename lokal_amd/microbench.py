@@ -1,0 +1,162 @@
+"""Measurements of the decode-step kernels on the workloads other than the
+headline one (bench.py measures config 3, Qwen2.5-0.5B-shape Q8_0 decode).
+
+    python -m lokal_amd.microbench [--only decode,layers,attn]
+
+Prints one JSON object per measurement:
+  decode  configs 1 and 4: SmolLM2-135M-shape F16 (512-token prompt, 128
+          greedy tokens) and TinyLlama-1.1B-shape Q4_K (256-token prompt, 256
+          tokens), tok/s with the algorithmic weight bytes and % of 8 TB/s;
+  layers  config 2: RMSNorm, RoPE-pair rotation, SwiGLU and the f16 embedding
+          gather at Qwen2.5-0.5B widths for 1, 8 and 64 rows (latency-bound:
+          µs and GB/s, no %-of-peak target);
+  attn    config 5: flash-decoding of 4 sequences, one query token each, at
+          contexts 4096 / 16384 / 32768 over 24 layers of f16 KV (14 q / 2 kv
+          heads), µs per step and HBM GB/s of the KV bytes read once.
+Kernel times come from hipEvents around repeated launches on one stream.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+
+import numpy as np
+
+from . import kernels as K
+from . import synth
+from .engine import Engine
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _timed(fn, reps: int, stream: K.Stream) -> float:
+    """Average ms of fn() over reps launches after two warm-ups."""
+    for _ in range(2):
+        fn()
+    a, b = K.Event(), K.Event()
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    stream.synchronize()
+    return a.elapsed_ms(b) / reps
+
+
+def decode(name: str, prompt_len: int, steps: int) -> dict:
+    cfg, tensors = synth.synth_named(name, 0)
+    eng = Engine.from_tensors(cfg, tensors)
+    del tensors
+    s = eng.session(prompt_len + steps + 16)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, prompt_len).astype(np.uint32)
+    lg = s.prefill(prompt)
+    tok = int(np.argmax(lg))
+    ids = s.decode_greedy(tok, prompt_len, 8)  # warm-up
+    t0 = time.perf_counter()
+    s.decode_greedy(int(ids[-1]), prompt_len + 8, steps)
+    dt = time.perf_counter() - t0
+    tok_s = steps / dt
+    wbytes = eng.matvec_bytes
+    gbs = wbytes * tok_s / 1e9
+    s.close()
+    eng.close()
+    return {"workload": name, "prompt": prompt_len, "decode_tokens": steps, "tok_s": round(tok_s, 1),
+            "ms_per_token": round(dt / steps * 1e3, 4), "weight_bytes_per_token": wbytes,
+            "weight_gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def layers() -> list[dict]:
+    st = K.Stream()
+    out = []
+    h, nq, inter, vocab = 896, 14, 4864, 151936
+    rng = np.random.default_rng(0)
+    table = K.Weight(synth.F16, vocab, h, synth.gen_weight(synth.F16, 0, "model.embed_tokens.weight", vocab, h).data)
+    for rows in (1, 8, 64):
+        x = K.DeviceArray.from_numpy(rng.standard_normal((rows, h)).astype(np.float32))
+        g = K.DeviceArray.from_numpy((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
+        y = K.DeviceArray((rows, h))
+        ms = _timed(lambda: K.rmsnorm(x, g, rows, h, 1e-6, y, st.ptr), 200, st)
+        nbytes = rows * h * 4 * 2 + h * 4
+        out.append({"kernel": "rmsnorm", "rows": rows, "n": h, "us": round(ms * 1e3, 3),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+        q = K.DeviceArray.from_numpy(rng.standard_normal((rows, nq * 64)).astype(np.float32))
+        pos = K.DeviceArray.from_numpy(rng.integers(0, 32768, rows).astype(np.uint32))
+        ms = _timed(lambda: K.rope_pairs(q, rows, nq * 64, 64, pos, 1e6, st.ptr), 200, st)
+        nbytes = rows * nq * 64 * 4 * 2 + rows * 4
+        out.append({"kernel": "rope_pairs", "rows": rows, "n": nq * 64, "us": round(ms * 1e3, 3),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+        gd = K.DeviceArray.from_numpy(rng.standard_normal(rows * inter).astype(np.float32))
+        ud = K.DeviceArray.from_numpy(rng.standard_normal(rows * inter).astype(np.float32))
+        od = K.DeviceArray(rows * inter)
+        ms = _timed(lambda: K.swiglu(gd, ud, rows * inter, od, st.ptr), 200, st)
+        nbytes = rows * inter * 4 * 3
+        out.append({"kernel": "swiglu", "rows": rows, "n": inter, "us": round(ms * 1e3, 3),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+        ids = K.DeviceArray.from_numpy(rng.integers(0, vocab, rows).astype(np.uint32))
+        eo = K.DeviceArray((rows, h))
+        ms = _timed(lambda: K.embed_gather(table, ids, rows, eo, st.ptr), 200, st)
+        nbytes = rows * h * (2 + 4) + rows * 4
+        out.append({"kernel": "embed_gather_f16", "rows": rows, "n": h, "us": round(ms * 1e3, 3),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    st.close()
+    return out
+
+
+def attn() -> list[dict]:
+    st = K.Stream()
+    out = []
+    n_seq, nh, nkv, hd, n_layers = 4, 14, 2, 64, 24
+    rng = np.random.default_rng(0)
+    for ctx in (4096, 16384, 32768):
+        # one layer's cache holds N(0,1) f16 values; the 24 layers of a step
+        # are 24 distinct caches, so every step reads the full KV once
+        kv_elems = n_seq * nkv * ctx * hd
+        caches = []
+        base = rng.standard_normal(kv_elems).astype(np.float16).view(np.uint16)
+        for layer in range(n_layers):
+            k = K.DeviceArray.from_numpy(np.roll(base, layer * 7919))
+            v = K.DeviceArray.from_numpy(np.roll(base, layer * 104729 + 1))
+            caches.append((k, v))
+        q = K.DeviceArray.from_numpy(rng.standard_normal((n_seq, nh * hd)).astype(np.float32))
+        cl = K.DeviceArray.from_numpy(np.full(n_seq, ctx, np.uint32))
+        o = K.DeviceArray((n_seq, nh * hd))
+
+        def step():
+            for k, v in caches:
+                K.attn_decode(q, k, v, cl, n_seq, nh, nkv, hd, ctx, o, st.ptr)
+
+        ms = _timed(step, 10, st)
+        nbytes = n_layers * n_seq * nkv * ctx * hd * 2 * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"workload": "attn-4seq", "ctx": ctx, "layers": n_layers, "us_per_step": round(ms * 1e3, 1),
+                    "kv_bytes_per_step": nbytes, "gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        for k, v in caches:
+            k.free()
+            v.free()
+    st.close()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", default="decode,layers,attn")
+    args = ap.parse_args()
+    want = set(args.only.split(","))
+    if K.device_count() == 0:
+        print("microbench: no HIP device visible", file=sys.stderr)
+        return 1
+    if "decode" in want:
+        print(json.dumps(decode("smollm2-135m", 512, 128)), flush=True)
+        print(json.dumps(decode("tinyllama-1.1b-q4_k", 256, 256)), flush=True)
+    if "layers" in want:
+        for r in layers():
+            print(json.dumps(r), flush=True)
+    if "attn" in want:
+        for r in attn():
+            print(json.dumps(r), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

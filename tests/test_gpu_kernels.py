@@ -225,6 +225,12 @@ def test_attention_long_context():
     _attn_case(2, 14, 2, [16384, 9999], 16384, seed=6)
 
 
+def test_attention_config5_four_sequences_32k():
+    """Long-context GQA flash-decoding at the Qwen2.5-0.5B shape: 4 sequences
+    with independent contexts up to 32768, one query token each."""
+    _attn_case(4, 14, 2, [32768, 32768, 16384, 4096], 32768, seed=7)
+
+
 def test_argmax_first_max_wins():
     x = np.random.default_rng(1).standard_normal((3, 151936)).astype(np.float32)
     x[1, 500] = x[1, 900] = 100.0
