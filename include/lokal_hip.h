@@ -121,6 +121,13 @@ int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_tensor* ten
  * (src/gpu/metal.rs:1667); config from GGUF metadata as gguf::model_config does
  * (src/gguf/arch.rs:164-223). */
 int lkhip_engine_create_gguf(const char* path, lkhip_engine** out);
+/* Parses a GGUF file's header and tensor table only (no device needed): the
+ * config lkhip_engine_create_gguf would build (gguf::model_config,
+ * src/gguf/arch.rs:164-227), the number of tensors the decode step reads
+ * (hf_name, src/gguf/arch.rs:229-270) and whether q/k rows carry the llama
+ * converter's permutation (load_f32, src/gguf/dequant.rs:538-557).  Errors
+ * as GgufFile::open reports them (src/gguf/container.rs:162-261). */
+int lkhip_gguf_config(const char* path, lkhip_config* cfg_out, size_t* n_tensors_out, int* llama_permuted_out);
 void lkhip_engine_destroy(lkhip_engine* e);
 /* Engine::config (src/engine.rs:15). */
 int lkhip_engine_config(const lkhip_engine* e, lkhip_config* out);

@@ -6,6 +6,6 @@ src/engine.rs:13-71) plus kernel-level bindings and synthetic checkpoints.
 """
 from ._lib import LokalHipError
 from .config import CONFIGS, ModelConfig
-from .engine import BatchRow, Batcher, Engine, Session, create
+from .engine import BatchRow, Batcher, Engine, Session, create, gguf_config
 
 __all__ = ["Engine", "Session", "Batcher", "BatchRow", "create", "ModelConfig", "CONFIGS", "LokalHipError"]

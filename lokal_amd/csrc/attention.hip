@@ -61,7 +61,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
     const KV* __restrict__ K = (const KV*)a.k + kv_base;
     const KV* __restrict__ V = (const KV*)a.v + kv_base;
-    constexpr bool KV32 = sizeof(KV) == 4;
 
     __shared__ float qs[G][LK_HD];
     __shared__ float ps[4][G][64];      // [wave][head][group * 8 + jj]

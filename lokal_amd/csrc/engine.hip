@@ -17,6 +17,7 @@
 #include "../../include/lokal_hip.h"
 #include "lkhip_common.h"
 #include "fused.h"
+#include "gguf.h"
 
 // ------------------------------------------------------------------ errors
 
@@ -1223,9 +1224,35 @@ extern "C" int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* o
     return LKHIP_OK;
 }
 
+extern "C" int lkhip_gguf_config(const char* path, lkhip_config* cfg_out, size_t* n_tensors_out,
+                                 int* llama_permuted_out) {
+    if (!path || !cfg_out) return fail(LKHIP_E_INVALID, "gguf_config: null argument");
+    LkGguf g;
+    std::string why;
+    const int rc = lk_gguf_open(path, &g, &why);
+    if (rc) return fail(rc, "%s", why.c_str());
+    *cfg_out = g.cfg;
+    if (n_tensors_out) *n_tensors_out = g.tensors.size();
+    if (llama_permuted_out) *llama_permuted_out = g.llama_permuted;
+    lk_gguf_close(&g);
+    return LKHIP_OK;
+}
+
 extern "C" int lkhip_engine_create_gguf(const char* path, lkhip_engine** out) {
-    (void)path;
-    if (out) *out = nullptr;
-    return fail(LKHIP_E_UNSUPPORTED, "GGUF file loading is not wired yet — build the engine from tensors "
-                                     "(lkhip_engine_create_tensors)");
+    if (!path || !out) return fail(LKHIP_E_INVALID, "engine: null argument");
+    *out = nullptr;
+    LkGguf g;
+    std::string why;
+    int rc = lk_gguf_open(path, &g, &why);
+    if (rc) return fail(rc, "%s", why.c_str());
+    // weights stay quantized: the engine repacks the mapped bytes onto the
+    // device (the create_metal_quant path, src/engine.rs:150-162)
+    std::vector<lkhip_tensor> ts(g.tensors.size());
+    for (size_t i = 0; i < g.tensors.size(); i++) {
+        const LkGgufTensor& t = g.tensors[i];
+        ts[i] = lkhip_tensor{t.name.c_str(), t.type, t.n_dims, {t.dims[0], t.dims[1]}, t.data, t.nbytes};
+    }
+    rc = lkhip_engine_create_tensors(&g.cfg, ts.data(), ts.size(), g.llama_permuted ? 1 : 0, out);
+    lk_gguf_close(&g);
+    return rc;
 }

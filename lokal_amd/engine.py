@@ -36,6 +36,19 @@ def _cfg_struct(cfg: ModelConfig) -> Config:
                   cfg.rms_norm_eps, cfg.rope_theta)
 
 
+def _cfg_from_struct(c: Config) -> ModelConfig:
+    return ModelConfig(c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
+                       c.num_key_value_heads, c.vocab_size, c.rms_norm_eps, c.rope_theta,
+                       c.max_position_embeddings, c.head_dim)
+
+
+def gguf_config(path: str) -> tuple[ModelConfig, int, bool]:
+    """Config, tensor count and llama-permutation flag of a GGUF file (no device needed)."""
+    c, n, perm = Config(), C.c_size_t(), C.c_int()
+    check(lib().lkhip_gguf_config(str(path).encode(), C.byref(c), C.byref(n), C.byref(perm)))
+    return _cfg_from_struct(c), int(n.value), bool(perm.value)
+
+
 def _f32p(a: np.ndarray):
     return a.ctypes.data_as(C.POINTER(C.c_float))
 
@@ -78,14 +91,12 @@ class Engine:
 
     @classmethod
     def from_gguf(cls, path: str) -> "Engine":
+        """engine::create_metal_quant's counterpart: weights stay quantized."""
         h = C.c_void_p()
         check(lib().lkhip_engine_create_gguf(str(path).encode(), C.byref(h)))
         c = Config()
         check(lib().lkhip_engine_config(h, C.byref(c)))
-        cfg = ModelConfig(c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
-                          c.num_key_value_heads, c.vocab_size, c.rms_norm_eps, c.rope_theta,
-                          c.max_position_embeddings, c.head_dim)
-        return cls(h, cfg)
+        return cls(h, _cfg_from_struct(c))
 
     def config(self) -> ModelConfig:
         return self.cfg
@@ -227,4 +238,4 @@ class Batcher:
         self.close()
 
 
-__all__ = ["Engine", "Session", "Batcher", "BatchRow", "create", "LokalHipError", "_lib"]
+__all__ = ["Engine", "Session", "Batcher", "BatchRow", "create", "gguf_config", "LokalHipError", "_lib"]

@@ -1,0 +1,150 @@
+"""The GGUF container reader (lkhip_gguf_config / lkhip_engine_create_gguf):
+header walk, metadata, alignment, dim reversal, names, bounds and refusals on
+the CPU (src/gguf/container.rs:162-261, src/gguf/arch.rs:164-270 and the
+reference's own container tests, whose tiny-file fixture is rebuilt here);
+on the GPU, an engine from a written file runs exactly like one from the
+same tensors."""
+import struct
+
+import numpy as np
+import pytest
+
+from tests.gguf_writer import write_gguf
+from lokal_amd import Engine, LokalHipError, gguf_config, synth
+from lokal_amd.config import ModelConfig
+
+TINY = ModelConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                   num_key_value_heads=2, vocab_size=300, rms_norm_eps=1e-6, rope_theta=1e6,
+                   max_position_embeddings=2048)
+
+
+def _tiny_fixture(version=3, align=None):
+    """One string KV, one Q8_0 tensor of ne=[32, 2] at offset 0 (the shape of
+    the reference's tiny_gguf fixture)."""
+    kv = b""
+    n_kv = 1 + (align is not None)
+
+    def s(x):
+        return struct.pack("<Q", len(x)) + x.encode()
+
+    kv += s("general.architecture") + struct.pack("<I", 8) + s("llama")
+    if align is not None:
+        kv += s("general.alignment") + struct.pack("<II", 4, align)
+    info = s("t") + struct.pack("<IQQIQ", 2, 32, 2, 8, 0)
+    b = b"GGUF" + struct.pack("<IQQ", version, 1, n_kv) + kv + info
+    a = align or 32
+    b += b"\0" * ((-len(b)) % a)
+    return b + b"\0" * 68
+
+
+def test_config_and_names_from_a_written_file(tmp_path):
+    tensors = synth.synth_model(TINY, synth.Q8_0, 1, tied=True, qkv_bias=True)
+    p = tmp_path / "m.gguf"
+    write_gguf(p, TINY, tensors, arch="qwen2")
+    cfg, n, permuted = gguf_config(p)
+    assert (cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers, cfg.num_attention_heads,
+            cfg.num_key_value_heads, cfg.vocab_size) == (256, 512, 2, 4, 2, 300)
+    assert cfg.rms_norm_eps == pytest.approx(1e-6) and cfg.rope_theta == pytest.approx(1e6)
+    assert cfg.max_position_embeddings == 2048
+    assert n == len(tensors) and not permuted
+
+
+def test_llama_arch_is_flagged_permuted_and_alignment_honoured(tmp_path):
+    tensors = synth.synth_model(TINY, synth.F16, 2, tied=False)
+    p = tmp_path / "l.gguf"
+    write_gguf(p, TINY, tensors, arch="llama", align=64, with_tokens=False,
+               extra_kv=[("llama.vocab_size", "u32", TINY.vocab_size)])
+    cfg, n, permuted = gguf_config(p)
+    assert permuted and cfg.vocab_size == 300 and n == len(tensors)
+
+
+def test_vocab_falls_back_to_the_embedding_rows(tmp_path):
+    tensors = synth.synth_model(TINY, synth.F16, 2, tied=True)
+    p = tmp_path / "v.gguf"
+    write_gguf(p, TINY, tensors, arch="llama", with_tokens=False)
+    assert gguf_config(p)[0].vocab_size == 300
+
+
+@pytest.mark.parametrize("align", [None, 16])
+def test_reference_tiny_fixture_parses_then_asks_for_the_config(tmp_path, align):
+    p = tmp_path / "t.gguf"
+    p.write_bytes(_tiny_fixture(3, align))
+    with pytest.raises(LokalHipError, match="llama.embedding_length is missing"):
+        gguf_config(p)
+
+
+def test_refusals(tmp_path):
+    p = tmp_path / "x.gguf"
+    p.write_bytes(b"GGML" + b"\0" * 60)
+    with pytest.raises(LokalHipError, match="bad magic"):
+        gguf_config(p)
+    p.write_bytes(_tiny_fixture(version=1))
+    with pytest.raises(LokalHipError, match="version 1 unsupported"):
+        gguf_config(p)
+    p.write_bytes(b"GGUF" + struct.pack(">I", 3) + b"\0" * 16)
+    with pytest.raises(LokalHipError, match="big-endian"):
+        gguf_config(p)
+    p.write_bytes(_tiny_fixture()[:40])
+    with pytest.raises(LokalHipError, match="truncated"):
+        gguf_config(p)
+    with pytest.raises(LokalHipError, match="cannot open"):
+        gguf_config(tmp_path / "missing.gguf")
+
+
+def test_unsupported_types_are_listed_together(tmp_path):
+    tensors = synth.synth_model(TINY, synth.Q8_0, 3, tied=True)
+    # relabel two matrices as Q6_K / Q5_K with sizes that fit those types
+    out = []
+    for t in tensors:
+        if t.name.endswith(("layers.0.mlp.down_proj.weight", "layers.1.mlp.down_proj.weight")):
+            rows, cols = t.dims
+            out.append(synth.Tensor(t.name, 14, t.dims, np.zeros(rows * cols // 256 * 210, np.uint8)))
+        elif t.name.endswith("layers.0.mlp.up_proj.weight"):
+            rows, cols = t.dims
+            out.append(synth.Tensor(t.name, 13, t.dims, np.zeros(rows * cols // 256 * 176, np.uint8)))
+        else:
+            out.append(t)
+    p = tmp_path / "u.gguf"
+    write_gguf(p, TINY, out)
+    with pytest.raises(LokalHipError, match=r"2 weight type\(s\).*across 3 of .*Q5_K \(1 tensor.*Q6_K \(2 tensors"):
+        gguf_config(p)
+
+
+def test_unsupported_architecture(tmp_path):
+    tensors = synth.synth_model(TINY, synth.F16, 2, tied=True)
+    p = tmp_path / "a.gguf"
+    write_gguf(p, TINY, tensors, arch="gemma")
+    with pytest.raises(LokalHipError, match='"gemma" is not supported'):
+        gguf_config(p)
+
+
+def test_tensor_past_the_end_is_refused(tmp_path):
+    tensors = synth.synth_model(TINY, synth.F16, 2, tied=True)
+    p = tmp_path / "e.gguf"
+    write_gguf(p, TINY, tensors)
+    b = p.read_bytes()
+    p.write_bytes(b[:-4096])
+    with pytest.raises(LokalHipError, match="run past the file"):
+        gguf_config(p)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arch,wtype,bias", [("qwen2", synth.Q8_0, True), ("llama", synth.Q4_K, False),
+                                             ("llama", synth.F16, False)])
+def test_engine_from_gguf_matches_engine_from_tensors(tmp_path, arch, wtype, bias):
+    cfg = TINY if wtype != synth.Q4_K else TINY.with_(hidden_size=512, intermediate_size=1024,
+                                                      num_attention_heads=8)
+    tensors = synth.synth_model(cfg, wtype, 5, tied=(arch == "qwen2"), qkv_bias=bias)
+    p = tmp_path / "g.gguf"
+    write_gguf(p, cfg, tensors, arch=arch)
+    a = Engine.from_gguf(str(p))
+    b = Engine.from_tensors(cfg, tensors)
+    assert a.cfg.vocab_size == cfg.vocab_size
+    sa, sb = a.session(64), b.session(64)
+    for pos, t in enumerate(np.random.default_rng(6).integers(0, cfg.vocab_size, 12)):
+        la, lb = sa.forward(int(t), pos), sb.forward(int(t), pos)
+        assert np.array_equal(la, lb), (arch, pos)
+    sa.close()
+    sb.close()
+    a.close()
+    b.close()
