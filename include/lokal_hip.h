@@ -179,6 +179,12 @@ int lkhip_batch_prefill(lkhip_batch* b, uint32_t slot, const uint32_t* ids, size
 /* Batcher::decode_step (src/engine.rs:46): one token per row; one weight read
  * serves every row.  logits_out holds n_rows * vocab floats, in row order. */
 int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, float* logits_out);
+/* The serve loop's greedy decode over a batch (generate.rs:101-118 at -t 0 per
+ * row, with Batcher::decode_step as the step, src/engine.rs:46): feeds each
+ * row's token at its pos, then each row's argmax back, n_steps times, all on
+ * the device; ids_out is n_steps * n_rows ids, step-major.  n_rows <= 64. */
+int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, size_t n_steps,
+                              uint32_t* ids_out);
 
 /* ------------------------------------------------------------ memory */
 
@@ -220,6 +226,13 @@ int lkhip_q8_0_matvec(const lkhip_weight* w, const float* x, const float* bias, 
                       void* stream);
 int lkhip_q4_k_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
                       void* stream);
+/* Linear::forward over n_rows activation rows (the multi-row GEMM of the
+ * batched path; lokal's Metal backend runs this as matmul_pg,
+ * src/gpu/kernels.metal:1749-1985): y[r*ldy + o] = dot(W[o,:], x[r*ldx ..])
+ * (+ bias[o]), or += with accumulate.  fp32 accumulation on the matrix cores.
+ * Needs cols % 32 == 0 (Q4_K: % 256), ldx % 4 == 0 and a 16-byte aligned x. */
+int lkhip_matmul(const lkhip_weight* w, const float* x, size_t n_rows, size_t ldx, const float* bias, float* y,
+                 size_t ldy, int accumulate, void* stream);
 /* math::rmsnorm (src/math.rs:45-49) over n_rows rows of n: y = x*s*w. */
 int lkhip_rmsnorm(const float* x, const float* w, size_t n_rows, size_t n, float eps, float* y, void* stream);
 /* model::rope (src/model.rs:268-279) in place on n_rows rows of n floats

@@ -88,6 +88,7 @@ SIGNATURES = {
     "lkhip_batch_destroy": (None, [_P]),
     "lkhip_batch_prefill": (C.c_int, [_P, C.c_uint32, _U32, C.c_size_t, _F]),
     "lkhip_batch_decode_step": (C.c_int, [_P, C.POINTER(Row), C.c_size_t, _F]),
+    "lkhip_batch_decode_greedy": (C.c_int, [_P, C.POINTER(Row), C.c_size_t, C.c_size_t, _U32]),
     "lkhip_malloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
     "lkhip_free": (C.c_int, [_P]),
     "lkhip_memcpy_htod": (C.c_int, [_P, _P, C.c_size_t]),
@@ -109,6 +110,7 @@ SIGNATURES = {
     "lkhip_matvec": (C.c_int, [_P, _P, _P, _P, C.c_int, _P]),
     "lkhip_q8_0_matvec": (C.c_int, [_P, _P, _P, _P, C.c_int, _P]),
     "lkhip_q4_k_matvec": (C.c_int, [_P, _P, _P, _P, C.c_int, _P]),
+    "lkhip_matmul": (C.c_int, [_P, _P, C.c_size_t, C.c_size_t, _P, _P, C.c_size_t, C.c_int, _P]),
     "lkhip_rmsnorm": (C.c_int, [_P, _P, C.c_size_t, C.c_size_t, C.c_float, _P, _P]),
     "lkhip_rope_pairs": (C.c_int, [_P, C.c_size_t, C.c_size_t, C.c_size_t, _P, C.c_float, _P]),
     "lkhip_swiglu": (C.c_int, [_P, _P, C.c_size_t, _P, _P]),

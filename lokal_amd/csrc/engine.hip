@@ -4,6 +4,7 @@
 // (src/model.rs:196-262), HIP-graph replay, and the kernel-level entry points.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -191,6 +192,14 @@ struct DevBuf {
     DevBuf(const DevBuf&) = delete;
     DevBuf& operator=(const DevBuf&) = delete;
     DevBuf(DevBuf&& o) noexcept : p(o.p) { o.p = nullptr; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        if (this != &o) {
+            if (p) (void)hipFree(p);
+            p = o.p;
+            o.p = nullptr;
+        }
+        return *this;
+    }
     ~DevBuf() {
         if (p) (void)hipFree(p);
     }
@@ -466,6 +475,32 @@ extern "C" double lkhip_engine_matvec_bytes(const lkhip_engine* e) { return e ? 
 
 // -------------------------------------------------------------- sessions
 
+// KV cache seen by the rows path: per layer [slot][n_kv][kv_seq][64].
+struct KvDesc {
+    uint8_t* kc = nullptr;
+    uint8_t* vc = nullptr;
+    size_t layer_bytes = 0;    // one layer of one cache, all slots
+    uint64_t slot_elems = 0;   // elements between two slots
+    uint32_t kv_seq = 0;       // cache rows per kv head
+    uint32_t max_seq = 0;      // positions a slot holds
+    int kv_f32 = 0;
+};
+
+enum HeadMode { HEAD_NONE = 0, HEAD_LAST = 1, HEAD_ALL = 2 };
+#define LK_ROWS_LOGITS 64u   // rows whose logits one pass can return
+#define LK_PREFILL_CHUNK 512u  // prompt positions per prefill pass (PREFILL_CHUNK, src/gpu/metal.rs:30)
+
+struct Rows {
+    uint32_t cap = 0;
+    DevBuf meta;   // u32 [ids | pos | slots | ctx | steps], cap each
+    DevBuf x, xn, qkv, att, inner, logits, gpart, apart, out_ids;
+    size_t out_ids_cap = 0;
+    uint32_t* h_meta = nullptr;  // pinned, 5 * cap
+    ~Rows() {
+        if (h_meta) (void)hipHostFree(h_meta);
+    }
+};
+
 enum Cat { C_MATVEC = 0, C_LMHEAD = 1, C_ATTN = 2, C_OTHER = 3 };
 
 struct lkhip_session {
@@ -486,6 +521,7 @@ struct lkhip_session {
     uint32_t max_chunks = 0;
     size_t fused_lds = 0;
     DevBuf xb, qb, pb, ab, xpb, ib, epoch;
+    std::unique_ptr<Rows> rows;  // multi-row buffers (prefill, forward_batch), on first use
     DevBuf trace;          // stage timestamps of one block (lkhip_session_set_trace)
     int trace_block = -1;
     // profiling
@@ -861,33 +897,6 @@ extern "C" int lkhip_session_forward(lkhip_session* s, uint32_t token, size_t po
     return copy_logits(s, logits_out);
 }
 
-extern "C" int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size_t n, float* logits_out) {
-    if (!s || (!ids && n)) return fail(LKHIP_E_INVALID, "prefill: null argument");
-    if (n == 0) return fail(LKHIP_E_INVALID, "empty prompt");
-    if (n > s->max_seq)
-        return fail(LKHIP_E_INVALID, "prompt (%zu tokens) exceeds the session's context (%zu)", n, s->max_seq);
-    for (size_t i = 0; i < n; i++)
-        if (ids[i] >= s->e->cfg.vocab_size)
-            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", ids[i], s->e->cfg.vocab_size);
-    int rc;
-    if (n > 1) HIP_OR_FAIL(hipMemcpyAsync(s->feed.p, ids + 1, (n - 1) * 4, hipMemcpyHostToDevice, s->stream));
-    if ((rc = set_state(s, ids[0], 0, (uint32_t)(n - 1)))) return rc;
-    for (size_t i = 0; i < n; i++)
-        if ((rc = run_step(s))) return rc;
-    if (logits_out) return copy_logits(s, logits_out);
-    return sync_check(s);
-}
-
-extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n, size_t pos0,
-                                           float* logits_out) {
-    if (!s || !ids || !logits_out) return fail(LKHIP_E_INVALID, "forward_batch: null argument");
-    for (size_t i = 0; i < n; i++) {
-        int rc = lkhip_session_forward(s, ids[i], pos0 + i, logits_out + i * (size_t)s->e->cfg.vocab_size);
-        if (rc) return rc;
-    }
-    return LKHIP_OK;
-}
-
 extern "C" int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, size_t pos, size_t n_steps,
                                            uint32_t* ids_out, float* logits_last) {
     if (!s || (!ids_out && n_steps)) return fail(LKHIP_E_INVALID, "decode_greedy: null argument");
@@ -997,50 +1006,491 @@ extern "C" int lkhip_session_trace(lkhip_session* s, uint64_t* ticks, size_t n) 
     return LKHIP_OK;
 }
 
+// ------------------------------------------------------------ rows path
+// Model::forward (src/model.rs:196-262) for B tokens in one pass: every
+// linear layer is one multi-row GEMM (gemm.hip) that reads each weight once
+// for all rows.  A row is (token, position, KV slot); rows of one slot at
+// consecutive positions are a prefill chunk (each row attends to the
+// positions up to its own: its K/V are written before attention runs), rows
+// of different slots are a Batcher decode step (src/engine.rs:42-47).
+
+// Split-K workspace the rows path needs for up to `cap` rows.
+static size_t rows_gemm_part(const lkhip_engine* e, uint32_t cap) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size;
+    size_t need = 0;
+    for (uint32_t n = 1; n <= cap; n++) {
+        const LkGemmPlan p[5] = {lk_gemm_plan(e->qd + 2 * e->kvd, h, n, LK_MV_STORE),
+                                 lk_gemm_plan(h, e->qd, n, LK_MV_ACC), lk_gemm_plan(I, h, n, LK_MV_SWIGLU),
+                                 lk_gemm_plan(h, I, n, LK_MV_ACC),
+                                 lk_gemm_plan(c.vocab_size, h, n < LK_ROWS_LOGITS ? n : LK_ROWS_LOGITS, LK_MV_STORE)};
+        for (const auto& q : p) need = std::max(need, q.part_floats);
+    }
+    return need;
+}
+
+static int rows_check_engine(const lkhip_engine* e) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size;
+    for (const Layer& ly : e->layers) {
+        if (!lk_gemm_shape_ok(ly.q->dw.type, e->qd + 2 * e->kvd, h) || !lk_gemm_shape_ok(ly.o->dw.type, h, e->qd) ||
+            !lk_gemm_shape_ok(ly.gate->dw.type, I, h) || !lk_gemm_shape_ok(ly.down->dw.type, h, I))
+            return fail(LKHIP_E_UNSUPPORTED,
+                        "the batched path needs hidden and intermediate widths that are multiples of 32 (256 for "
+                        "Q4_K) — hidden %u, intermediate %u do not fit",
+                        h, I);
+    }
+    return LKHIP_OK;
+}
+
+static int rows_alloc(const lkhip_engine* e, Rows& R, uint32_t cap, uint32_t max_seq) {
+    const lkhip_config& c = e->cfg;
+    int rc = rows_check_engine(e);
+    if (rc) return rc;
+    R.cap = cap;
+    const size_t h = c.hidden_size, I = c.intermediate_size, qkvd = e->qd + 2 * e->kvd;
+    const size_t lrows = std::min<uint32_t>(cap, LK_ROWS_LOGITS);
+    if ((rc = dev_alloc(R.meta, 5 * (size_t)cap * 4)) || (rc = dev_alloc(R.x, cap * h * 4)) ||
+        (rc = dev_alloc(R.xn, cap * h * 4)) || (rc = dev_alloc(R.qkv, cap * qkvd * 4)) ||
+        (rc = dev_alloc(R.att, cap * (size_t)e->qd * 4)) || (rc = dev_alloc(R.inner, cap * I * 4)) ||
+        (rc = dev_alloc(R.logits, lrows * c.vocab_size * 4)) ||
+        (rc = dev_alloc(R.gpart, rows_gemm_part(e, cap) * 4)) ||
+        (rc = dev_alloc(R.apart, lk_attn_part_floats(cap, c.num_attention_heads, max_seq) * 4)))
+        return rc;
+    HIP_OR_FAIL(hipHostMalloc((void**)&R.h_meta, 5 * (size_t)cap * 4, hipHostMallocDefault));
+    return LKHIP_OK;
+}
+
+static hipError_t rows_gemm(Rows& R, LkGemmArgs a, int mode, hipStream_t st) {
+    a.part = R.gpart.as<float>();
+    a.ks = 0;  // the planned split
+    return lk_gemm_launch(a, mode, st);
+}
+
+// One pass over n rows whose meta is already on the device; logits of the
+// last row (HEAD_LAST) or of every row (HEAD_ALL, n <= LK_ROWS_LOGITS).
+static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const KvDesc& kv, int head,
+                               hipStream_t st) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size, qd = e->qd, kvd = e->kvd;
+    const uint32_t qkvd = qd + 2 * kvd, cap = R.cap;
+    uint32_t* meta = R.meta.as<uint32_t>();
+    const uint32_t *ids = meta, *pos = meta + cap, *slots = meta + 2 * cap, *ctx = meta + 3 * cap;
+    float *x = R.x.as<float>(), *xn = R.xn.as<float>(), *qkv = R.qkv.as<float>();
+    float *att = R.att.as<float>(), *inner = R.inner.as<float>();
+    hipError_t err;
+#define RSTEP(call)                                   \
+    do {                                              \
+        if ((err = (call)) != hipSuccess) return err; \
+    } while (0)
+    RSTEP(lk_gather_launch(e->embed->dw, ids, n, x, st));
+    for (uint32_t L = 0; L < c.num_hidden_layers; L++) {
+        const Layer& ly = e->layers[L];
+        RSTEP(lk_rmsnorm_launch(x, ly.in_norm.as<float>(), n, h, c.rms_norm_eps, xn, st));
+        {
+            LkGemmArgs a{};
+            a.nseg = 3;
+            a.seg[0] = {ly.q->dw, ly.has_bias ? ly.bq.as<float>() : nullptr, qkv};
+            a.seg[1] = {ly.k->dw, ly.has_bias ? ly.bk.as<float>() : nullptr, qkv + qd};
+            a.seg[2] = {ly.v->dw, ly.has_bias ? ly.bv.as<float>() : nullptr, qkv + qd + kvd};
+            a.N = qkvd;
+            a.K = h;
+            a.n_rows = n;
+            a.x = xn;
+            a.ldx = h;
+            a.ldy = qkvd;
+            RSTEP(rows_gemm(R, a, LK_MV_STORE, st));
+        }
+        uint8_t* kc = kv.kc + L * kv.layer_bytes;
+        uint8_t* vc = kv.vc + L * kv.layer_bytes;
+        RSTEP(lk_rope_kv_launch(qkv, c.num_attention_heads, c.num_key_value_heads, e->freq, nullptr, pos, n, kc, vc,
+                                kv.kv_f32, kv.kv_seq, kv.slot_elems, slots, st));
+        {
+            LkAttnArgs a{};
+            a.q = qkv;
+            a.k = kc;
+            a.v = vc;
+            a.kv_f32 = (uint32_t)kv.kv_f32;
+            a.out = att;
+            a.part = R.apart.as<float>();
+            a.ctx_len = ctx;
+            a.slots = slots;
+            a.n_seq = n;
+            a.n_heads = c.num_attention_heads;
+            a.n_kv = c.num_key_value_heads;
+            a.max_seq = kv.kv_seq;
+            a.seq_stride = kv.slot_elems;
+            a.q_stride = qkvd;
+            RSTEP(lk_attn_launch(a, st));
+        }
+        {
+            LkGemmArgs a{};
+            a.nseg = 1;
+            a.seg[0] = {ly.o->dw, nullptr, x};
+            a.N = h;
+            a.K = qd;
+            a.n_rows = n;
+            a.x = att;
+            a.ldx = qd;
+            a.ldy = h;
+            RSTEP(rows_gemm(R, a, LK_MV_ACC, st));
+        }
+        RSTEP(lk_rmsnorm_launch(x, ly.post_norm.as<float>(), n, h, c.rms_norm_eps, xn, st));
+        {
+            LkGemmArgs a{};
+            a.nseg = 2;
+            a.seg[0] = {ly.gate->dw, nullptr, inner};
+            a.seg[1] = {ly.up->dw, nullptr, nullptr};
+            a.N = I;
+            a.K = h;
+            a.n_rows = n;
+            a.x = xn;
+            a.ldx = h;
+            a.ldy = I;
+            RSTEP(rows_gemm(R, a, LK_MV_SWIGLU, st));
+        }
+        {
+            LkGemmArgs a{};
+            a.nseg = 1;
+            a.seg[0] = {ly.down->dw, nullptr, x};
+            a.N = h;
+            a.K = I;
+            a.n_rows = n;
+            a.x = inner;
+            a.ldx = I;
+            a.ldy = h;
+            RSTEP(rows_gemm(R, a, LK_MV_ACC, st));
+        }
+    }
+    if (head != HEAD_NONE) {
+        const uint32_t hr = head == HEAD_ALL ? n : 1;
+        const float* xs = head == HEAD_ALL ? x : x + (size_t)(n - 1) * h;
+        RSTEP(lk_rmsnorm_launch(xs, e->norm.as<float>(), hr, h, c.rms_norm_eps, xn, st));
+        LkGemmArgs a{};
+        a.nseg = 1;
+        a.seg[0] = {e->lm_head->dw, nullptr, R.logits.as<float>()};
+        a.N = c.vocab_size;
+        a.K = h;
+        a.n_rows = hr;
+        a.x = xn;
+        a.ldx = h;
+        a.ldy = c.vocab_size;
+        RSTEP(rows_gemm(R, a, LK_MV_STORE, st));
+    }
+#undef RSTEP
+    return hipSuccess;
+}
+
+// Uploads n rows of (token, pos, slot) (ctx = pos + 1, steps = 0).
+static int rows_upload(Rows& R, const uint32_t* tok, const size_t* pos, const uint32_t* slot, uint32_t n,
+                       hipStream_t st) {
+    const uint32_t cap = R.cap;
+    // the pinned buffer may still feed an earlier async copy
+    HIP_OR_FAIL(hipStreamSynchronize(st));
+    for (uint32_t i = 0; i < n; i++) {
+        R.h_meta[i] = tok[i];
+        R.h_meta[cap + i] = (uint32_t)pos[i];
+        R.h_meta[2 * cap + i] = slot[i];
+        R.h_meta[3 * cap + i] = (uint32_t)pos[i] + 1;
+        R.h_meta[4 * cap + i] = 0;
+    }
+    for (int a = 0; a < 5; a++)
+        HIP_OR_FAIL(hipMemcpyAsync(R.meta.as<uint32_t>() + (size_t)a * cap, R.h_meta + (size_t)a * cap, n * 4,
+                                   hipMemcpyHostToDevice, st));
+    return LKHIP_OK;
+}
+
+// Prefill of ids at positions pos0.. into one slot, in chunks; the logits of
+// the last position into logits_out (device -> host), if given.
+static int rows_prefill(const lkhip_engine* e, Rows& R, const KvDesc& kv, uint32_t slot, const uint32_t* ids,
+                        size_t n, size_t pos0, float* logits_out, hipStream_t st) {
+    const uint32_t chunk = std::min<uint32_t>(R.cap, LK_PREFILL_CHUNK);
+    std::vector<size_t> pos(chunk);
+    std::vector<uint32_t> slots(chunk, slot);
+    for (size_t off = 0; off < n; off += chunk) {
+        const uint32_t m = (uint32_t)std::min<size_t>(chunk, n - off);
+        for (uint32_t i = 0; i < m; i++) pos[i] = pos0 + off + i;
+        int rc = rows_upload(R, ids + off, pos.data(), slots.data(), m, st);
+        if (rc) return rc;
+        const bool last = off + m == n;
+        hipError_t err = enqueue_rows(e, R, m, kv, last && logits_out ? HEAD_LAST : HEAD_NONE, st);
+        if (err != hipSuccess) return fail(LKHIP_E_HIP, "batched prefill launch failed: %s", hipGetErrorString(err));
+    }
+    if (logits_out)
+        HIP_OR_FAIL(hipMemcpyAsync(logits_out, R.logits.p, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, st));
+    HIP_OR_FAIL(hipStreamSynchronize(st));
+    return LKHIP_OK;
+}
+
+static KvDesc session_kv(lkhip_session* s) {
+    KvDesc d;
+    const size_t el = s->kv_f32 ? 4 : 2;
+    d.kc = s->kc.as<uint8_t>();
+    d.vc = s->vc.as<uint8_t>();
+    d.layer_bytes = kv_layer_elems(s) * el;
+    d.slot_elems = 0;
+    d.kv_seq = (uint32_t)s->kv_seq;
+    d.max_seq = (uint32_t)s->max_seq;
+    d.kv_f32 = s->kv_f32;
+    return d;
+}
+
+// The session's rows buffers, allocated on first use.
+static int session_rows(lkhip_session* s) {
+    if (s->rows) return LKHIP_OK;
+    auto r = std::make_unique<Rows>();
+    const uint32_t cap = (uint32_t)std::min<size_t>(s->max_seq, LK_PREFILL_CHUNK);
+    int rc = rows_alloc(s->e, *r, cap, (uint32_t)s->kv_seq);
+    if (rc) return rc;
+    s->rows = std::move(r);
+    return LKHIP_OK;
+}
+
+// LKHIP_PREFILL=loop runs prefill as the per-token decode step instead.
+static bool prefill_batched() {
+    const char* p = getenv("LKHIP_PREFILL");
+    return !(p && strcmp(p, "loop") == 0);
+}
+
+extern "C" int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size_t n, float* logits_out) {
+    if (!s || (!ids && n)) return fail(LKHIP_E_INVALID, "prefill: null argument");
+    if (n == 0) return fail(LKHIP_E_INVALID, "empty prompt");
+    if (n > s->max_seq)
+        return fail(LKHIP_E_INVALID, "prompt (%zu tokens) exceeds the session's context (%zu)", n, s->max_seq);
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= s->e->cfg.vocab_size)
+            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", ids[i], s->e->cfg.vocab_size);
+    int rc;
+    if (prefill_batched() && rows_check_engine(s->e) == LKHIP_OK) {
+        if ((rc = session_rows(s))) return rc;
+        return rows_prefill(s->e, *s->rows, session_kv(s), 0, ids, n, 0, logits_out, s->stream);
+    }
+    if (n > 1) HIP_OR_FAIL(hipMemcpyAsync(s->feed.p, ids + 1, (n - 1) * 4, hipMemcpyHostToDevice, s->stream));
+    if ((rc = set_state(s, ids[0], 0, (uint32_t)(n - 1)))) return rc;
+    for (size_t i = 0; i < n; i++)
+        if ((rc = run_step(s))) return rc;
+    if (logits_out) return copy_logits(s, logits_out);
+    return sync_check(s);
+}
+
+extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n, size_t pos0,
+                                           float* logits_out) {
+    if (!s || (!ids && n) || (!logits_out && n)) return fail(LKHIP_E_INVALID, "forward_batch: null argument");
+    if (n == 0) return LKHIP_OK;
+    if (pos0 + n > s->max_seq)
+        return fail(LKHIP_E_INVALID, "positions %zu..%zu exceed the session's KV cache (%zu positions)", pos0,
+                    pos0 + n - 1, s->max_seq);
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= s->e->cfg.vocab_size)
+            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", ids[i], s->e->cfg.vocab_size);
+    int rc = rows_check_engine(s->e);
+    if (rc) {  // widths the GEMM does not take: the token loop
+        for (size_t i = 0; i < n; i++)
+            if ((rc = lkhip_session_forward(s, ids[i], pos0 + i, logits_out + i * (size_t)s->e->cfg.vocab_size)))
+                return rc;
+        return LKHIP_OK;
+    }
+    if ((rc = session_rows(s))) return rc;
+    Rows& R = *s->rows;
+    const size_t V = s->e->cfg.vocab_size;
+    const uint32_t chunk = std::min<uint32_t>(R.cap, LK_ROWS_LOGITS);
+    std::vector<size_t> pos(chunk);
+    std::vector<uint32_t> slots(chunk, 0);
+    const KvDesc kv = session_kv(s);
+    for (size_t off = 0; off < n; off += chunk) {
+        const uint32_t m = (uint32_t)std::min<size_t>(chunk, n - off);
+        for (uint32_t i = 0; i < m; i++) pos[i] = pos0 + off + i;
+        if ((rc = rows_upload(R, ids + off, pos.data(), slots.data(), m, s->stream))) return rc;
+        hipError_t err = enqueue_rows(s->e, R, m, kv, HEAD_ALL, s->stream);
+        if (err != hipSuccess) return fail(LKHIP_E_HIP, "forward_batch launch failed: %s", hipGetErrorString(err));
+        HIP_OR_FAIL(hipMemcpyAsync(logits_out + off * V, R.logits.p, m * V * 4, hipMemcpyDeviceToHost, s->stream));
+    }
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    return LKHIP_OK;
+}
+
 // ------------------------------------------------------------------ batcher
-// Continuous batching seam (src/engine.rs:42-47).  One session per slot; a
-// decode step advances each row through its slot's session.
+// Continuous batching (src/engine.rs:36-47): a KV pool of n_slots slots,
+// per layer [slot][n_kv][kv_seq][64] f16; a decode step is one rows pass over
+// the step's rows (one weight read for all of them).  Decode steps of a given
+// row count are captured once as a HIP graph and replayed.
 
 struct lkhip_batch {
     lkhip_engine* e = nullptr;
-    std::vector<lkhip_session*> slots;
+    size_t n_slots = 0, max_seq = 0;
+    hipStream_t stream = nullptr;
+    DevBuf kc, vc;
+    KvDesc kv;
+    Rows rows;
+    std::vector<hipGraphExec_t> step_graph;    // by row count: logits of every row
+    std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
     ~lkhip_batch() {
-        for (auto* s : slots) lkhip_session_destroy(s);
+        for (auto g : step_graph)
+            if (g) (void)hipGraphExecDestroy(g);
+        for (auto g : greedy_graph)
+            if (g) (void)hipGraphExecDestroy(g);
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (stream) (void)hipStreamDestroy(stream);
     }
 };
 
+static bool graphs_on() {
+    const char* g = getenv("LKHIP_GRAPH");
+    return !(g && g[0] == '0');
+}
+
+// Enqueues a decode step of n rows (meta on the device); greedy adds the
+// argmax feedback.  Replays a captured graph when graphs are on.
+static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy) {
+    std::vector<hipGraphExec_t>& cache = greedy ? b->greedy_graph : b->step_graph;
+    auto body = [&](hipStream_t st) -> hipError_t {
+        hipError_t err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        if (err != hipSuccess || !greedy) return err;
+        return lk_rows_greedy_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.meta.as<uint32_t>(),
+                                     b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
+    };
+    if (!graphs_on()) {
+        hipError_t err = body(b->stream);
+        if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode_step launch failed: %s", hipGetErrorString(err));
+        return LKHIP_OK;
+    }
+    if (cache.size() <= n) cache.resize(n + 1, nullptr);
+    if (!cache[n]) {
+        HIP_OR_FAIL(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal));
+        hipError_t e1 = body(b->stream);
+        hipGraph_t g = nullptr;
+        hipError_t e2 = hipStreamEndCapture(b->stream, &g);
+        if (e1 != hipSuccess || e2 != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return fail(LKHIP_E_HIP, "capturing the batched decode step failed: %s",
+                        hipGetErrorString(e1 != hipSuccess ? e1 : e2));
+        }
+        hipError_t e3 = hipGraphInstantiate(&cache[n], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e3 != hipSuccess) {
+            cache[n] = nullptr;
+            return fail(LKHIP_E_HIP, "instantiating the batched decode step failed: %s", hipGetErrorString(e3));
+        }
+    }
+    HIP_OR_FAIL(hipGraphLaunch(cache[n], b->stream));
+    return LKHIP_OK;
+}
+
 extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_seq, lkhip_batch** out) {
-    if (!e || !out || n_slots == 0) return fail(LKHIP_E_INVALID, "batch: bad argument");
+    if (!e || !out || n_slots == 0 || max_seq == 0) return fail(LKHIP_E_INVALID, "batch: bad argument");
+    if (max_seq > 0x7FFFFFFF || n_slots > 4096) return fail(LKHIP_E_INVALID, "batch: max_seq or n_slots too large");
     *out = nullptr;
+    (void)hipSetDevice(e->device);
     auto b = std::make_unique<lkhip_batch>();
     b->e = e;
-    for (size_t i = 0; i < n_slots; i++) {
-        lkhip_session* s = nullptr;
-        int rc = lkhip_session_create(e, max_seq, &s);
-        if (rc) return rc;
-        b->slots.push_back(s);
-    }
+    b->n_slots = n_slots;
+    b->max_seq = max_seq;
+    const lkhip_config& c = e->cfg;
+    const size_t kv_seq = (max_seq + 63) / 64 * 64;
+    const uint64_t slot_elems = (uint64_t)c.num_key_value_heads * kv_seq * 64;
+    const size_t layer_bytes = n_slots * slot_elems * 2;
+    int rc;
+    HIP_OR_FAIL(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
+    if ((rc = dev_alloc(b->kc, c.num_hidden_layers * layer_bytes)) ||
+        (rc = dev_alloc(b->vc, c.num_hidden_layers * layer_bytes)))
+        return rc;
+    b->kv.kc = b->kc.as<uint8_t>();
+    b->kv.vc = b->vc.as<uint8_t>();
+    b->kv.layer_bytes = layer_bytes;
+    b->kv.slot_elems = slot_elems;
+    b->kv.kv_seq = (uint32_t)kv_seq;
+    b->kv.max_seq = (uint32_t)max_seq;
+    b->kv.kv_f32 = 0;
+    const uint32_t cap = (uint32_t)std::max<size_t>(n_slots, std::min<size_t>(max_seq, LK_PREFILL_CHUNK));
+    if ((rc = rows_alloc(e, b->rows, cap, (uint32_t)kv_seq))) return rc;
     *out = b.release();
     return LKHIP_OK;
 }
 extern "C" void lkhip_batch_destroy(lkhip_batch* b) { delete b; }
+
 extern "C" int lkhip_batch_prefill(lkhip_batch* b, uint32_t slot, const uint32_t* ids, size_t n, float* logits_out) {
-    if (!b || slot >= b->slots.size()) return fail(LKHIP_E_INVALID, "batch prefill: slot out of range");
-    return lkhip_session_prefill(b->slots[slot], ids, n, logits_out);
+    if (!b || (!ids && n)) return fail(LKHIP_E_INVALID, "batch prefill: null argument");
+    if (slot >= b->n_slots) return fail(LKHIP_E_INVALID, "batch prefill: slot %u out of range", slot);
+    if (n == 0) return fail(LKHIP_E_INVALID, "empty prompt");
+    if (n > b->max_seq)
+        return fail(LKHIP_E_INVALID, "prompt (%zu tokens) exceeds the slot's context (%zu)", n, b->max_seq);
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= b->e->cfg.vocab_size)
+            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", ids[i], b->e->cfg.vocab_size);
+    return rows_prefill(b->e, b->rows, b->kv, slot, ids, n, 0, logits_out, b->stream);
 }
-extern "C" int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, float* logits_out) {
-    if (!b || (!rows && n_rows) || (!logits_out && n_rows)) return fail(LKHIP_E_INVALID, "decode_step: null argument");
+
+static int batch_check_rows(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, size_t extra_steps) {
+    if (n_rows > b->n_slots) return fail(LKHIP_E_INVALID, "decode_step: %zu rows for %zu slots", n_rows, b->n_slots);
     for (size_t i = 0; i < n_rows; i++) {
-        if (rows[i].slot >= b->slots.size()) return fail(LKHIP_E_INVALID, "decode_step: slot %u out of range", rows[i].slot);
+        if (rows[i].slot >= b->n_slots)
+            return fail(LKHIP_E_INVALID, "decode_step: slot %u out of range", rows[i].slot);
+        if (rows[i].token >= b->e->cfg.vocab_size)
+            return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", rows[i].token,
+                        b->e->cfg.vocab_size);
+        if (rows[i].pos + extra_steps >= b->max_seq)
+            return fail(LKHIP_E_INVALID, "position %llu exceeds the slot's KV cache (%zu positions)",
+                        (unsigned long long)(rows[i].pos + extra_steps), b->max_seq);
         for (size_t j = 0; j < i; j++)
             if (rows[j].slot == rows[i].slot)
                 return fail(LKHIP_E_INVALID, "decode_step: slot %u appears twice in one step", rows[i].slot);
     }
-    for (size_t i = 0; i < n_rows; i++) {
-        int rc = lkhip_session_forward(b->slots[rows[i].slot], rows[i].token, rows[i].pos,
-                                       logits_out + i * (size_t)b->e->cfg.vocab_size);
-        if (rc) return rc;
+    return LKHIP_OK;
+}
+
+static int batch_upload_rows(lkhip_batch* b, const lkhip_row* rows, uint32_t n) {
+    std::vector<uint32_t> tok(n), slot(n);
+    std::vector<size_t> pos(n);
+    for (uint32_t i = 0; i < n; i++) {
+        tok[i] = rows[i].token;
+        slot[i] = rows[i].slot;
+        pos[i] = (size_t)rows[i].pos;
     }
+    return rows_upload(b->rows, tok.data(), pos.data(), slot.data(), n, b->stream);
+}
+
+extern "C" int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, float* logits_out) {
+    if (!b || (!rows && n_rows) || (!logits_out && n_rows)) return fail(LKHIP_E_INVALID, "decode_step: null argument");
+    if (n_rows == 0) return LKHIP_OK;
+    int rc = batch_check_rows(b, rows, n_rows, 0);
+    if (rc) return rc;
+    const size_t V = b->e->cfg.vocab_size;
+    for (size_t off = 0; off < n_rows; off += LK_ROWS_LOGITS) {  // logits of up to 64 rows per pass
+        const uint32_t m = (uint32_t)std::min<size_t>(LK_ROWS_LOGITS, n_rows - off);
+        if ((rc = batch_upload_rows(b, rows + off, m)) || (rc = batch_enqueue_step(b, m, false))) return rc;
+        HIP_OR_FAIL(hipMemcpyAsync(logits_out + off * V, b->rows.logits.p, m * V * 4, hipMemcpyDeviceToHost, b->stream));
+    }
+    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
+    return LKHIP_OK;
+}
+
+extern "C" int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, size_t n_steps,
+                                         uint32_t* ids_out) {
+    if (!b || (!rows && n_rows) || (!ids_out && n_rows && n_steps))
+        return fail(LKHIP_E_INVALID, "decode_greedy: null argument");
+    if (n_rows == 0 || n_steps == 0) return LKHIP_OK;
+    if (n_rows > LK_ROWS_LOGITS)
+        return fail(LKHIP_E_INVALID, "decode_greedy: %zu rows — one call takes at most %u", n_rows, LK_ROWS_LOGITS);
+    int rc = batch_check_rows(b, rows, n_rows, n_steps - 1);
+    if (rc) return rc;
+    const uint32_t n = (uint32_t)n_rows;
+    const size_t need = n_steps * n_rows;
+    if (need > b->rows.out_ids_cap) {  // the greedy graphs hold the buffer's address
+        HIP_OR_FAIL(hipStreamSynchronize(b->stream));
+        for (auto& g : b->greedy_graph)
+            if (g) {
+                (void)hipGraphExecDestroy(g);
+                g = nullptr;
+            }
+        b->rows.out_ids = DevBuf();
+        if ((rc = dev_alloc(b->rows.out_ids, need * 4))) return rc;
+        b->rows.out_ids_cap = need;
+    }
+    if ((rc = batch_upload_rows(b, rows, n))) return rc;
+    for (size_t s = 0; s < n_steps; s++)
+        if ((rc = batch_enqueue_step(b, n, true))) return rc;
+    HIP_OR_FAIL(hipMemcpyAsync(ids_out, b->rows.out_ids.p, need * 4, hipMemcpyDeviceToHost, b->stream));
+    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
     return LKHIP_OK;
 }
 
@@ -1142,6 +1592,39 @@ extern "C" int lkhip_q4_k_matvec(const lkhip_weight* w, const float* x, const fl
                                  void* stream) {
     if (w && w->dw.type != LKHIP_Q4_K) return fail(LKHIP_E_INVALID, "q4_k_matvec: weight is %s", type_name(w->dw.type));
     return lkhip_matvec(w, x, bias, y, accumulate, stream);
+}
+
+extern "C" int lkhip_matmul(const lkhip_weight* w, const float* x, size_t n_rows, size_t ldx, const float* bias,
+                            float* y, size_t ldy, int accumulate, void* stream) {
+    if (!w || ((!x || !y) && n_rows)) return fail(LKHIP_E_INVALID, "matmul: null argument");
+    if (n_rows == 0) return LKHIP_OK;
+    if (n_rows > 0xFFFF) return fail(LKHIP_E_INVALID, "matmul: at most 65535 rows per call");
+    const LkDevW& d = w->dw;
+    if (!lk_gemm_shape_ok(d.type, d.rows, d.cols))
+        return fail(LKHIP_E_UNSUPPORTED, "matmul: a %ux%u %s weight does not fit the GEMM (cols %% %u)", d.rows,
+                    d.cols, type_name(d.type), d.type == LKHIP_Q4_K ? 256u : 32u);
+    if (ldx < d.cols || ldy < d.rows || ldx % 4 || (uintptr_t)x % 16)
+        return fail(LKHIP_E_INVALID, "matmul: ldx must be >= cols and a multiple of 4, x 16-byte aligned, ldy >= rows");
+    const int mode = accumulate ? LK_MV_ACC : LK_MV_STORE;
+    const LkGemmPlan p = lk_gemm_plan(d.rows, d.cols, (uint32_t)n_rows, mode);
+    hipStream_t st = (hipStream_t)stream;
+    void* part = nullptr;
+    if (p.part_floats) HIP_OR_FAIL(hipMallocAsync(&part, p.part_floats * 4, st));
+    LkGemmArgs a{};
+    a.nseg = 1;
+    a.seg[0] = {d, bias, y};
+    a.N = d.rows;
+    a.K = d.cols;
+    a.n_rows = (uint32_t)n_rows;
+    a.x = x;
+    a.ldx = (uint32_t)ldx;
+    a.ldy = (uint32_t)ldy;
+    a.part = (float*)part;
+    a.ks = p.ks;
+    hipError_t e = lk_gemm_launch(a, mode, st);
+    if (part) (void)hipFreeAsync(part, st);
+    if (e != hipSuccess) return fail(LKHIP_E_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    return LKHIP_OK;
 }
 
 extern "C" int lkhip_rmsnorm(const float* x, const float* w, size_t n_rows, size_t n, float eps, float* y,

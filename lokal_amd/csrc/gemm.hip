@@ -1,0 +1,361 @@
+// gemm.hip -- the multi-row dequant-fused linear layer on the matrix cores:
+// Y[b][n] = sum_k X[b][k] * W[n][k] (+ bias[n]) for b < B rows of f32
+// activations, W in its GGUF type (F16, Q8_0, Q4_K) dequantized as it is
+// loaded.  This is Linear::forward (src/model.rs:27-35) applied to a batch of
+// tokens: the Batcher's decode step (one row per sequence, src/engine.rs:42-47)
+// and chunked prefill (rows = prompt positions of one sequence), the work
+// lokal's Metal backend gives matmul_pg (src/gpu/kernels.metal:1749-1985).
+//
+// Arithmetic: v_mfma_f32_16x16x4f32 -- fp32 operands, fp32 accumulation.
+// Dequantized weights are exact f32 values (int8 * f16 scale, 4-bit Q4_K with
+// the reference's two roundings, f16), so the only difference from the CPU
+// path's dot (src/math.rs:10-38) is the summation order.
+//
+// Work split:
+//   wave   = 16 weight rows x 16*MB batch rows, over a range of K chunks
+//            (segments of a multi-segment launch hold whole 16-row tiles);
+//   block  = 4 waves on 64 consecutive weight rows sharing one X tile;
+//   chunk  = 128 columns of K: lane l takes weight row (l & 15) and the 32
+//            consecutive columns 32*(l >> 4) .. +31 of the chunk, so a row's
+//            128 columns are one contiguous run fetched by 4 lanes, and a
+//            Q8_0 lane holds exactly one 32-weight block (one scale);
+//   MFMA t (t = 0..31) multiplies every lane's t-th weight with the X value of
+//            the same column: the lane-group/column map is a permutation of
+//            k shared by both operands, so the product is the plain dot.
+// X chunks are staged in LDS (double-buffered, one barrier per chunk) and
+// shared by the block's 4 waves; the next chunk's weights and X are loaded
+// before the current chunk's MFMAs.  Small matrices split K over the grid
+// (blockIdx.z); their partial tiles go to a workspace and gemm_reduce_kernel
+// sums them in a fixed order and runs the epilogue.
+#include "lkhip_common.h"
+#include "matvec_impl.h"
+
+namespace lkg {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t KC = 128;   // K columns per chunk
+constexpr uint32_t XS = KC + 4;  // LDS row stride of the X tile (floats)
+
+template <int WT> struct Raw;
+template <> struct Raw<LK_Q8_0> { uint4 q[2]; uint32_t d; };
+template <> struct Raw<LK_F16> { uint4 q[4]; };
+template <> struct Raw<LK_Q4_K> { uint4 q[2]; uint4 hd; };
+
+// Raw bytes of the 32 weights (row r, columns kb..kb+31) of one lane.
+template <int WT>
+__device__ __forceinline__ void raw_load(Raw<WT>& R, const LkDevW& w, uint32_t r, uint32_t kb) {
+    if constexpr (WT == LK_Q8_0) {
+        const uint4* p = (const uint4*)(w.data + (size_t)r * w.cols + kb);
+        R.q[0] = p[0];
+        R.q[1] = p[1];
+        R.d = ((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + kb / 32];
+    } else if constexpr (WT == LK_F16) {
+        const uint4* p = (const uint4*)(w.data + ((size_t)r * w.cols + kb) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) R.q[i] = p[i];
+    } else {
+        const uint32_t nsb = w.cols / 256, sb = kb / 256, g = (kb % 256) / 64;
+        const uint4* p = (const uint4*)(w.data + ((size_t)r * nsb + sb) * 128 + 32 * g);
+        R.q[0] = p[0];
+        R.q[1] = p[1];
+        R.hd = *(const uint4*)(w.aux + ((size_t)r * nsb + sb) * 16);
+    }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Weights 8*s .. 8*s+7 of the lane's 32 as exact f32 (dequant_row_ref,
+// src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K); zero when
+// the lane's columns lie past K.
+template <int WT>
+__device__ __forceinline__ void dequant8(const Raw<WT>& R, int s, uint32_t kb, bool ok, float* w) {
+    if constexpr (WT == LK_Q8_0) {
+        const float d = ok ? lk_h2f((uint16_t)R.d) : 0.f;
+        const uint4 v = R.q[s >> 1];
+        const uint32_t w0 = word_of(v, (s & 1) * 2), w1 = word_of(v, (s & 1) * 2 + 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            w[t] = __fmul_rn((float)((int32_t)(w0 << (24 - 8 * t)) >> 24), d);
+            w[4 + t] = __fmul_rn((float)((int32_t)(w1 << (24 - 8 * t)) >> 24), d);
+        }
+    } else if constexpr (WT == LK_F16) {
+        const uint4 v = R.q[s];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = word_of(v, i);
+            w[2 * i] = ok ? lk_h2f((uint16_t)(x & 0xFFFF)) : 0.f;
+            w[2 * i + 1] = ok ? lk_h2f((uint16_t)(x >> 16)) : 0.f;
+        }
+    } else {
+        // sub-block is = (kb % 256) / 32: low nibbles for even, high for odd
+        const uint32_t is = (kb % 256) / 32;
+        const float d = lk_h2f((uint16_t)(R.hd.x & 0xFFFF));
+        const float dmin = lk_h2f((uint16_t)(R.hd.x >> 16));
+        uint32_t sc, m;
+        lk::scale_min_k4(is, R.hd.y, R.hd.z, R.hd.w, sc, m);
+        const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
+        const uint4 v = R.q[s >> 1];
+        const uint32_t sh = (is & 1) * 4;
+        const uint32_t w0 = word_of(v, (s & 1) * 2), w1 = word_of(v, (s & 1) * 2 + 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t q0 = (w0 >> (8 * t + sh)) & 15u, q1 = (w1 >> (8 * t + sh)) & 15u;
+            w[t] = ok ? __fsub_rn(__fmul_rn(d1, (float)q0), m1) : 0.f;
+            w[4 + t] = ok ? __fsub_rn(__fmul_rn(d1, (float)q1), m1) : 0.f;
+        }
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// Epilogue of one output element: segment n (global index over segments).
+__device__ __forceinline__ void emit(const LkGemmArgs& a, int mode, uint32_t b, uint32_t n, float v, float u) {
+    if (mode == LK_MV_SWIGLU) {
+        a.seg[0].out[(size_t)b * a.ldy + n] = silu_mul(v, u);
+        return;
+    }
+    uint32_t si = 0, nb = 0;
+    while (si + 1 < a.nseg && n >= nb + a.seg[si].w.rows) {
+        nb += a.seg[si].w.rows;
+        si++;
+    }
+    const LkSeg& s = a.seg[si];
+    const uint32_t nl = n - nb;
+    if (s.bias) v += s.bias[nl];
+    float* o = s.out + (size_t)b * a.ldy + nl;
+    if (mode == LK_MV_ACC) *o += v;
+    else *o = v;
+}
+
+template <int WT, int MB, int MODE>
+__global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
+    constexpr bool SW = MODE == LK_MV_SWIGLU;
+    constexpr int BR = 16 * MB;  // batch rows of the block tile
+    __shared__ float xs[2][BR * XS];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t n0 = (blockIdx.x * 4 + wave) * 16;
+    const bool live = n0 < a.N;  // wave-uniform; dead waves still stage X
+    const uint32_t B = a.n_rows, K = a.K;
+    const uint32_t b0 = blockIdx.y * BR;
+    const uint32_t nck = (K + KC - 1) / KC;
+    const uint32_t per = (nck + a.ks - 1) / a.ks;
+    const uint32_t c_begin = blockIdx.z * per;
+    const uint32_t c_end = c_begin + per < nck ? c_begin + per : nck;
+    const uint32_t j = (uint32_t)lane >> 4;
+
+    // weight row of this lane (segment lookup is wave-uniform: segments hold
+    // whole 16-row tiles)
+    uint32_t si = 0, nb = 0;
+    if constexpr (!SW) {
+        while (si + 1 < a.nseg && n0 >= nb + a.seg[si].w.rows) {
+            nb += a.seg[si].w.rows;
+            si++;
+        }
+    }
+    const LkDevW W0 = a.seg[si].w;
+    const LkDevW W1 = a.seg[SW ? 1 : si].w;
+    // rows past the last (a ragged final tile) re-read the last row; their
+    // outputs are not stored
+    uint32_t r = live ? n0 - nb + ((uint32_t)lane & 15) : 0;
+    r = r < W0.rows ? r : W0.rows - 1;
+
+    // X staging: thread t loads float4 number t + 256*i of the BR x KC tile
+    constexpr int XV = BR * KC / 4 / 256;  // float4 per thread per chunk
+    float4 xv[XV];
+    auto x_fetch = [&](uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + 256u * i;  // float4 index in the tile
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            uint32_t bb = b0 + row;
+            bb = bb < B ? bb : B - 1;
+            const uint32_t k = c * KC + col;
+            xv[i] = k < K ? *(const float4*)(a.x + (size_t)bb * a.ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto x_store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            *(float4*)&xs[buf][row * XS + col] = xv[i];
+        }
+    };
+    auto kb_of = [&](uint32_t c) -> uint32_t {
+        const uint32_t kb = c * KC + 32 * j;
+        return kb < K ? kb : K - 32;
+    };
+
+    f4 acc[MB], accu[SW ? MB : 1];
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (SW) accu[m] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    Raw<WT> cur, nxt, curu, nxtu;
+    if (c_begin < c_end) {
+        x_fetch(c_begin);
+        x_store(0);
+        if (live) {
+            raw_load(cur, W0, r, kb_of(c_begin));
+            if constexpr (SW) raw_load(curu, W1, r, kb_of(c_begin));
+        }
+    }
+    for (uint32_t c = c_begin; c < c_end; c++) {
+        const int buf = (int)((c - c_begin) & 1);
+        __syncthreads();  // X tile of chunk c is in xs[buf]
+        const bool more = c + 1 < c_end;
+        if (more) {
+            x_fetch(c + 1);
+            if (live) {
+                raw_load(nxt, W0, r, kb_of(c + 1));
+                if constexpr (SW) raw_load(nxtu, W1, r, kb_of(c + 1));
+            }
+        }
+        if (live) {
+            const uint32_t kb = kb_of(c);
+            const bool ok = c * KC + 32 * j < K;
+            const float* xrow = &xs[buf][((uint32_t)lane & 15) * XS + 32 * j];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float w[8], wu[8];
+                dequant8<WT>(cur, s, kb, ok, w);
+                if constexpr (SW) dequant8<WT>(curu, s, kb, ok, wu);
+                float xb[MB][8];
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    const float4 p = *(const float4*)(xrow + m * 16 * XS + 8 * s);
+                    const float4 q = *(const float4*)(xrow + m * 16 * XS + 8 * s + 4);
+                    xb[m][0] = p.x; xb[m][1] = p.y; xb[m][2] = p.z; xb[m][3] = p.w;
+                    xb[m][4] = q.x; xb[m][5] = q.y; xb[m][6] = q.z; xb[m][7] = q.w;
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+#pragma unroll
+                    for (int m = 0; m < MB; m++) {
+                        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[t], xb[m][t], acc[m], 0, 0, 0);
+                        if constexpr (SW)
+                            accu[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(wu[t], xb[m][t], accu[m], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        if (more) {
+            x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
+            cur = nxt;
+            if constexpr (SW) curu = nxtu;
+        }
+    }
+    if (!live) return;
+
+    // D layout of the 16x16 tile: lane holds rows n0 + 4j + i (i = 0..3) of
+    // column b = lane & 15.
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        const uint32_t b = b0 + 16u * m + ((uint32_t)lane & 15);
+        if (b >= B) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t n = n0 + 4 * j + i;
+            if (n >= a.N) continue;
+            const float v = acc[m][i];
+            const float u = SW ? accu[m][i] : 0.f;
+            if (a.ks == 1) {
+                emit(a, MODE, b, n, v, u);
+            } else {
+                const size_t np = SW ? 2 * (size_t)a.N : a.N;
+                float* p = a.part + ((size_t)blockIdx.z * B + b) * np;
+                p[n] = v;
+                if constexpr (SW) p[a.N + n] = u;
+            }
+        }
+    }
+}
+
+// Sums the K-split partials of element (b, n) in split order, then the epilogue.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, int mode) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (n >= a.N) return;
+    const bool sw = mode == LK_MV_SWIGLU;
+    const size_t np = sw ? 2 * (size_t)a.N : a.N;
+    float v = 0.f, u = 0.f;
+    for (uint32_t z = 0; z < a.ks; z++) {
+        const float* p = a.part + ((size_t)z * a.n_rows + b) * np;
+        v += p[n];
+        if (sw) u += p[a.N + n];
+    }
+    emit(a, mode, b, n, v, u);
+}
+
+template <int WT, int MB>
+hipError_t launch_mb(const LkGemmArgs& a, int mode, dim3 grid, hipStream_t st) {
+    switch (mode) {
+    case LK_MV_STORE: hipLaunchKernelGGL((gemm_kernel<WT, MB, LK_MV_STORE>), grid, dim3(256), 0, st, a); break;
+    case LK_MV_ACC: hipLaunchKernelGGL((gemm_kernel<WT, MB, LK_MV_ACC>), grid, dim3(256), 0, st, a); break;
+    case LK_MV_SWIGLU: hipLaunchKernelGGL((gemm_kernel<WT, MB, LK_MV_SWIGLU>), grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int WT>
+hipError_t launch_t(const LkGemmArgs& a, int mode, uint32_t mb, dim3 grid, hipStream_t st) {
+    if (mb == 1) return launch_mb<WT, 1>(a, mode, grid, st);
+    if (mb == 2) return launch_mb<WT, 2>(a, mode, grid, st);
+    return launch_mb<WT, 2>(a, mode, grid, st);
+}
+
+}  // namespace lkg
+
+static uint32_t gemm_mb(uint32_t n_rows) { return n_rows <= 16 ? 1 : 2; }
+
+LkGemmPlan lk_gemm_plan(uint32_t N, uint32_t K, uint32_t n_rows, int mode) {
+    LkGemmPlan p{};
+    p.mb = gemm_mb(n_rows);
+    const uint32_t gx = (N + 63) / 64, gy = (n_rows + 16 * p.mb - 1) / (16 * p.mb);
+    const uint32_t nck = (K + lkg::KC - 1) / lkg::KC;
+    // enough blocks for 2 per CU; every split keeps at least one chunk
+    uint32_t ks = (512 + gx * gy - 1) / (gx * gy);
+    if (ks > nck) ks = nck;
+    if (ks < 1) ks = 1;
+    const uint32_t per = (nck + ks - 1) / ks;
+    p.ks = (nck + per - 1) / per;
+    p.part_floats = p.ks > 1 ? (size_t)p.ks * n_rows * N * (mode == LK_MV_SWIGLU ? 2 : 1) : 0;
+    return p;
+}
+
+bool lk_gemm_shape_ok(uint32_t type, uint32_t N, uint32_t K) {
+    if (N == 0 || K == 0 || K % 32) return false;
+    if (type == LK_Q4_K && K % 256) return false;
+    return type == LK_Q8_0 || type == LK_F16 || type == LK_Q4_K;
+}
+
+hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st) {
+    const uint32_t type = a.seg[0].w.type;
+    if (a.n_rows == 0) return hipSuccess;
+    if (!lk_gemm_shape_ok(type, a.N, a.K) || (mode != LK_MV_STORE && mode != LK_MV_ACC && mode != LK_MV_SWIGLU))
+        return hipErrorInvalidValue;
+    for (uint32_t i = 0; i < a.nseg; i++)
+        if (a.seg[i].w.type != type || a.seg[i].w.cols != a.K) return hipErrorInvalidValue;
+    // a wave's 16-row tile lies in one segment
+    if (mode != LK_MV_SWIGLU)
+        for (uint32_t i = 0; i + 1 < a.nseg; i++)
+            if (a.seg[i].w.rows % 16) return hipErrorInvalidValue;
+    if (a.ldx % 4 || (size_t)(uintptr_t)a.x % 16) return hipErrorInvalidValue;  // float4 X loads
+    const LkGemmPlan p = lk_gemm_plan(a.N, a.K, a.n_rows, mode);
+    if (a.ks == 0) a.ks = p.ks;
+    if (a.ks > 1 && !a.part) return hipErrorInvalidValue;
+    dim3 grid((a.N + 63) / 64, (a.n_rows + 16 * p.mb - 1) / (16 * p.mb), a.ks);
+    hipError_t e;
+    switch (type) {
+    case LK_Q8_0: e = lkg::launch_t<LK_Q8_0>(a, mode, p.mb, grid, st); break;
+    case LK_F16: e = lkg::launch_t<LK_F16>(a, mode, p.mb, grid, st); break;
+    default: e = lkg::launch_t<LK_Q4_K>(a, mode, p.mb, grid, st); break;
+    }
+    if (e != hipSuccess || a.ks == 1) return e;
+    hipLaunchKernelGGL(lkg::gemm_reduce_kernel, dim3((a.N + 255) / 256, a.n_rows), dim3(256), 0, st, a, mode);
+    return hipGetLastError();
+}

@@ -213,3 +213,40 @@ hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepSt
     hipLaunchKernelGGL(step_finish_kernel, dim3(1), dim3(1024), 0, st, keys, n_keys, st_dev, feed_ids, ids_out);
     return hipGetLastError();
 }
+
+// Greedy step of a batch of sequences (generate.rs:101-118 at -t 0, one row
+// per sequence): row r's argmax (src/sampler.rs:67-75, first max wins) is
+// recorded as that row's next output id and fed back as its next token at the
+// next position.  meta holds u32 arrays [ids | pos | slots | ctx | steps],
+// each `cap` long; out_ids is [step][n_rows].
+__global__ __launch_bounds__(1024) void rows_greedy_kernel(const float* __restrict__ logits, uint32_t n,
+                                                           uint32_t* __restrict__ meta, uint32_t cap,
+                                                           uint32_t n_rows, uint32_t* __restrict__ out_ids) {
+    const uint32_t r = blockIdx.x;
+    const float* xr = logits + (size_t)r * n;
+    uint64_t k = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t kk = lk_argmax_key(xr[i], i);
+        k = kk > k ? kk : k;
+    }
+    k = max_key_block(k);
+    if (threadIdx.x == 0) {
+        const uint32_t id = lk_argmax_idx(k);
+        uint32_t* ids = meta;
+        uint32_t* pos = meta + cap;
+        uint32_t* ctx = meta + 3 * cap;
+        uint32_t* steps = meta + 4 * cap;
+        out_ids[(size_t)steps[r] * n_rows + r] = id;
+        steps[r] += 1;
+        ids[r] = id;
+        pos[r] += 1;
+        ctx[r] = pos[r] + 1;
+    }
+}
+
+hipError_t lk_rows_greedy_launch(const float* logits, uint32_t n_rows, uint32_t n, uint32_t* meta, uint32_t cap,
+                                 uint32_t* out_ids, hipStream_t st) {
+    if (n_rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rows_greedy_kernel, dim3(n_rows), dim3(1024), 0, st, logits, n, meta, cap, n_rows, out_ids);
+    return hipGetLastError();
+}

@@ -182,3 +182,34 @@ struct LkAttnArgs {
 uint32_t lk_attn_chunk(uint32_t max_seq);
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);
 hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st);
+
+// Multi-row dequant-fused GEMM (gemm.hip): Y[b][n] = sum_k X[b][k] W[n][k]
+// for b < n_rows, the B-row form of the matvec (Linear::forward over a batch
+// of tokens, src/model.rs:27-35).  Segments split N as in LkMvArgs (QKV); in
+// LK_MV_SWIGLU mode seg[0] is gate and seg[1] up, both N rows, and seg[0].out
+// receives silu(gate) * up.  Output row stride ldy (floats), input ldx.
+struct LkGemmArgs {
+    LkSeg seg[3];
+    uint32_t nseg;
+    uint32_t N;        // output units over all segments (SWIGLU: rows of one)
+    uint32_t K;
+    uint32_t n_rows;   // batch rows B
+    const float* x;
+    uint32_t ldx, ldy;
+    float* part;       // split-K partials [ks][n_rows][N or 2N]
+    uint32_t ks;       // K splits (1: the epilogue runs in the GEMM kernel)
+};
+// Plan: K splits for a launch and the partial floats it needs.
+struct LkGemmPlan {
+    uint32_t ks;
+    uint32_t mb;       // 16-row batch tiles per wave (1, 2 or 4)
+    size_t part_floats;
+};
+LkGemmPlan lk_gemm_plan(uint32_t N, uint32_t K, uint32_t n_rows, int mode);
+// Checks the shape the GEMM assumes: N a multiple of 16 per segment, K of 32.
+bool lk_gemm_shape_ok(uint32_t type, uint32_t N, uint32_t K);
+hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st);
+// Batched greedy step (layer.hip): argmax of each logits row fed back into the
+// row's token / position (meta = [ids | pos | slots | ctx | steps], cap each).
+hipError_t lk_rows_greedy_launch(const float* logits, uint32_t n_rows, uint32_t n, uint32_t* meta, uint32_t cap,
+                                 uint32_t* out_ids, hipStream_t st);

@@ -226,6 +226,14 @@ class Batcher:
         check(lib().lkhip_batch_decode_step(self._h, arr, len(rows), _f32p(out)))
         return [out[i] for i in range(len(rows))]
 
+    def decode_greedy(self, rows, n_steps: int) -> np.ndarray:
+        """Greedy decode of every row for n_steps steps on the device; returns
+        the [n_steps, n_rows] argmax ids."""
+        arr = (Row * len(rows))(*[Row(r.token, r.slot, r.pos) for r in rows])
+        out = np.empty((n_steps, len(rows)), dtype=np.uint32)
+        check(lib().lkhip_batch_decode_greedy(self._h, arr, len(rows), n_steps, _u32p(out)))
+        return out
+
     def close(self):
         if self._h:
             lib().lkhip_batch_destroy(self._h)

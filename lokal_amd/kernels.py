@@ -100,6 +100,13 @@ def matvec(w: Weight, x: DeviceArray, y: DeviceArray, bias: DeviceArray | None =
     check(lib().lkhip_matvec(w._h, x.ptr, _p(bias), y.ptr, int(accumulate), stream))
 
 
+def matmul(w: Weight, x: DeviceArray, n_rows: int, y: DeviceArray, bias: DeviceArray | None = None,
+           accumulate=False, ldx: int | None = None, ldy: int | None = None, stream=None) -> None:
+    """y[r, :rows] (+)= W x[r, :cols] (+ bias) for n_rows rows (multi-row GEMM)."""
+    check(lib().lkhip_matmul(w._h, x.ptr, n_rows, ldx or w.cols, _p(bias), y.ptr, ldy or w.rows, int(accumulate),
+                             stream))
+
+
 def q8_0_matvec(w, x, y, bias=None, accumulate=False, stream=None) -> None:
     check(lib().lkhip_q8_0_matvec(w._h, x.ptr, _p(bias), y.ptr, int(accumulate), stream))
 

@@ -1,0 +1,259 @@
+"""The multi-row path through the C ABI: the matrix-core GEMM (lkhip_matmul),
+chunked prefill and forward_batch of a Session, and the Batcher's decode step
+and device greedy loop, against the CPU oracle (lokal's CPU path restated).
+
+The GEMM is pinned three ways: a one-hot activation row returns a weight
+column bit-for-bit (every other product is an exact zero, so this fixes the
+lane/row/column index maps of the MFMA tiles), random rows agree with a
+float64 product of the oracle's dequantized weights to fp32 rounding, and
+split-K, bias, residual accumulation and row strides are exercised at the
+model widths.  End to end, logits are within 1e-3 relative error of the
+oracle (summation order is the only difference) and greedy ids agree."""
+import numpy as np
+import pytest
+
+import oracle
+from lokal_amd import BatchRow, Engine, LokalHipError, synth
+from lokal_amd import kernels as K
+from lokal_amd.config import ModelConfig
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TOL_F16_KV = TOL + 2.0 ** -10
+
+
+def rel_err(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def dequant(t, data, rows, cols):
+    return oracle.dequant_row(t, data, rows * cols).reshape(rows, cols)
+
+
+SHAPES = [  # (type, rows, cols)
+    (synth.Q8_0, 896, 896), (synth.Q8_0, 1152, 896), (synth.Q8_0, 896, 4864), (synth.Q8_0, 4864, 896),
+    (synth.F16, 576, 576), (synth.F16, 1536, 576), (synth.F16, 576, 1536),
+    (synth.Q4_K, 2048, 2048), (synth.Q4_K, 2048, 5632), (synth.Q4_K, 256, 512),
+]
+
+
+@pytest.mark.parametrize("t,rows,cols", SHAPES)
+def test_matmul_one_hot_is_bit_exact(t, rows, cols):
+    data = synth.gen_weight(t, 7, f"w{rows}x{cols}", rows, cols).data
+    w = K.Weight(t, rows, cols, data)
+    ref = dequant(t, data, rows, cols)
+    cols_hit = np.array([0, 1, 31, 32, 127, 128, cols // 2 + 3, cols - 1])
+    n = len(cols_hit)
+    x = np.zeros((n, cols), np.float32)
+    x[np.arange(n), cols_hit] = 1.0
+    xd, y = K.DeviceArray.from_numpy(x), K.DeviceArray((n, rows))
+    K.matmul(w, xd, n, y)
+    got = y.numpy()
+    for i, c in enumerate(cols_hit):
+        assert np.array_equal(got[i], ref[:, c]), (i, c)
+
+
+@pytest.mark.parametrize("t,rows,cols", SHAPES)
+@pytest.mark.parametrize("n_rows", [1, 5, 16, 17, 40])
+def test_matmul_matches_float64(t, rows, cols, n_rows):
+    data = synth.gen_weight(t, 3, f"w{rows}x{cols}", rows, cols).data
+    w = K.Weight(t, rows, cols, data)
+    ref = dequant(t, data, rows, cols).astype(np.float64)
+    rng = np.random.default_rng(n_rows)
+    x = rng.standard_normal((n_rows, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    y0 = rng.standard_normal((n_rows, rows)).astype(np.float32)
+    xd, bd = K.DeviceArray.from_numpy(x), K.DeviceArray.from_numpy(bias)
+    y = K.DeviceArray.from_numpy(y0)
+    K.matmul(w, xd, n_rows, y, bias=bd)
+    want = x.astype(np.float64) @ ref.T + bias
+    got = y.numpy()
+    # fp32 accumulation over cols products: relative to the row's |terms| sum
+    scale = np.abs(x).astype(np.float64) @ np.abs(ref).T
+    assert np.max(np.abs(got - want) / (scale + 1e-30)) < 1e-6
+    assert rel_err(got, want) < 1e-5
+    # residual accumulation (src/model.rs:235-237)
+    y.upload(y0)
+    K.matmul(w, xd, n_rows, y, accumulate=True)
+    assert rel_err(y.numpy(), y0 + x.astype(np.float64) @ ref.T) < 1e-5
+
+
+def test_matmul_row_strides():
+    t, rows, cols, n = synth.Q8_0, 896, 896, 7
+    data = synth.gen_weight(t, 5, "w", rows, cols).data
+    w = K.Weight(t, rows, cols, data)
+    ref = dequant(t, data, rows, cols).astype(np.float64)
+    x = np.random.default_rng(1).standard_normal((n, cols + 32)).astype(np.float32)
+    y = K.DeviceArray((n, rows + 48))
+    y.zero()
+    K.matmul(w, K.DeviceArray.from_numpy(x), n, y, ldx=cols + 32, ldy=rows + 48)
+    got = y.numpy()
+    assert rel_err(got[:, :rows], x[:, :cols].astype(np.float64) @ ref.T) < 1e-5
+    assert not got[:, rows:].any()
+
+
+def test_matmul_ragged_rows_and_refusals():
+    """A row count off the 16-row tile (a vocabulary like 1000) is computed and
+    nothing past the last row is written; strides it cannot load are refused."""
+    t, rows, cols, n = synth.Q8_0, 1000, 64, 3
+    data = synth.gen_weight(t, 1, "w", rows, cols).data
+    w = K.Weight(t, rows, cols, data)
+    x = np.random.default_rng(2).standard_normal((n, cols)).astype(np.float32)
+    y = K.DeviceArray((n, rows + 8))
+    y.upload(np.full((n, rows + 8), 7.0, np.float32))
+    K.matmul(w, K.DeviceArray.from_numpy(x), n, y, ldy=rows + 8)
+    got = y.numpy()
+    assert rel_err(got[:, :rows], x.astype(np.float64) @ dequant(t, data, rows, cols).T) < 1e-5
+    assert np.all(got[:, rows:] == 7.0)
+    with pytest.raises(LokalHipError, match="multiple of 4"):
+        K.matmul(w, K.DeviceArray((n, 70)), n, y, ldx=66)
+
+
+KINDS = {
+    "q8_0": dict(cfg=ModelConfig(896, 4864, 3, 14, 2, 1000, 1e-6, 1e6), weight_type=synth.Q8_0, tied=True,
+                 qkv_bias=True),
+    "q4_k": dict(cfg=ModelConfig(2048, 5632, 2, 32, 4, 1008, 1e-5, 1e4), weight_type=synth.Q4_K, tied=False,
+                 qkv_bias=False),
+    "f16": dict(cfg=ModelConfig(576, 1536, 3, 9, 3, 1008, 1e-5, 1e4), weight_type=synth.F16, tied=True,
+                qkv_bias=False),
+}
+
+
+def build(kind, seed=0):
+    k = KINDS[kind]
+    cfg = k["cfg"]
+    tensors = synth.synth_model(cfg, k["weight_type"], seed, tied=k["tied"], qkv_bias=k["qkv_bias"])
+    return cfg, Engine.from_tensors(cfg, tensors), oracle.Model(cfg, tensors)
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n", [1, 37, 600])
+def test_chunked_prefill_matches_oracle(kind, n):
+    """Prefill through the rows path (512-position chunks) against the CPU
+    path's token loop: last logits within 1e-3, every KV row of layer 0 within
+    one f16 ulp (f16 cache) or 1e-5 (f32 cache)."""
+    cfg, eng, om = build(kind, seed=2)
+    prompt = np.random.default_rng(n).integers(0, cfg.vocab_size, n).astype(np.uint32)
+    for kv in ("f32", "f16"):
+        s, o = eng.session(n + 4, kv_dtype=kv), om.session(n + 4, kv_f16=(kv == "f16"))
+        lg, lo = s.prefill(prompt), o.prefill(prompt)
+        assert rel_err(lg, lo) < (TOL if kv == "f32" else TOL_F16_KV), (kv, rel_err(lg, lo))
+        for pos in sorted({0, n // 2, n - 1}):
+            for which_v in (False, True):
+                got, want = s.read_kv(0, pos, which_v), o.kv(0, pos, which_v)
+                if kv == "f32":
+                    assert rel_err(got, want) < 1e-5
+                else:  # one f16 step, or fp32 noise on the row's scale
+                    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+                    excess = float(np.max(np.abs(got - want) - ulp - 1e-5 * np.max(np.abs(want))))
+                    assert excess <= 0.0, (pos, which_v, excess)
+        # decode continues from the batched prefill's cache
+        t = int(np.argmax(lo))
+        assert rel_err(s.forward(t, n), o.forward(t, n)) < (TOL if kv == "f32" else TOL_F16_KV)
+        s.close()
+        o.close()
+    eng.close()
+    om.close()
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+def test_forward_batch_matches_oracle_per_position(kind):
+    cfg, eng, om = build(kind, seed=4)
+    ids = np.random.default_rng(4).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    s, o = eng.session(80, kv_dtype="f32"), om.session(80)
+    got = s.forward_batch(ids[:10], 0)  # one pass
+    got = np.concatenate([got, s.forward_batch(ids[10:], 10)])  # 64 + 6 rows
+    for pos, t in enumerate(ids):
+        assert rel_err(got[pos], o.forward(int(t), pos)) < TOL, pos
+    s.close()
+    o.close()
+    eng.close()
+    om.close()
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+def test_batcher_decode_step_matches_independent_sequences(kind):
+    """Rows of different slots, lengths and positions in one step: each row's
+    logits equal the oracle's for its own sequence (src/engine.rs:42-47)."""
+    cfg, eng, om = build(kind, seed=5)
+    rng = np.random.default_rng(5)
+    lens = (5, 130, 1, 64)
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    bat = eng.batcher(len(lens), 256)
+    orc = [om.session(256, kv_f16=True) for _ in lens]
+    for slot, p in enumerate(prompts):
+        assert rel_err(bat.prefill(slot, p), orc[slot].prefill(p)) < TOL_F16_KV
+    pos = list(lens)
+    for step in range(3):
+        order = [(step + i) % len(lens) for i in range(len(lens))][: len(lens) - (step == 1)]
+        rows = [BatchRow(int(rng.integers(0, cfg.vocab_size)), pos[s], s) for s in order]
+        outs = bat.decode_step(rows)
+        for r, out in zip(rows, outs):
+            assert rel_err(out, orc[r.slot].forward(r.token, r.pos)) < TOL_F16_KV, (step, r.slot)
+            pos[r.slot] += 1
+    bat.close()
+    eng.close()
+    om.close()
+
+
+def test_batcher_greedy_matches_per_sequence_greedy():
+    """lkhip_batch_decode_greedy: every row's ids equal that sequence's own
+    greedy ids from a per-sequence decode_step loop with host argmax, and the
+    oracle's ids up to a near-tie within tolerance."""
+    cfg, eng, om = build("q8_0", seed=6)
+    rng = np.random.default_rng(6)
+    lens = (17, 3, 40)
+    steps = 24
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    bat = eng.batcher(len(lens), 128)
+    ref = eng.batcher(len(lens), 128)
+    first = []
+    for slot, p in enumerate(prompts):
+        lg = bat.prefill(slot, p)
+        ref.prefill(slot, p)
+        first.append(int(np.argmax(lg)))
+    rows = [BatchRow(first[s], lens[s], s) for s in range(len(lens))]
+    ids = bat.decode_greedy(rows, steps)
+    assert ids.shape == (steps, len(lens))
+    cur = list(first)
+    for k in range(steps):
+        outs = ref.decode_step([BatchRow(cur[s], lens[s] + k, s) for s in range(len(lens))])
+        cur = [int(oracle.argmax(o)) for o in outs]
+        assert list(ids[k]) == cur, k
+    # against the CPU path, row by row
+    for s, p in enumerate(prompts):
+        o = om.session(128, kv_f16=True)
+        lo = o.prefill(p)
+        t, agree = int(oracle.argmax(lo)), 0
+        for k in range(steps):
+            t = int(oracle.argmax(o.forward(t, lens[s] + k)))
+            if t != ids[k, s]:
+                break
+            agree += 1
+        o.close()
+        print(f"slot {s}: {agree}/{steps} greedy ids agree with the CPU path")
+        assert agree >= steps // 2
+    bat.close()
+    ref.close()
+    eng.close()
+    om.close()
+
+
+def test_batcher_refusals():
+    cfg, eng, om = build("q8_0")
+    bat = eng.batcher(2, 16)
+    with pytest.raises(LokalHipError, match="out of range"):
+        bat.decode_step([BatchRow(1, 0, 2)])
+    with pytest.raises(LokalHipError, match="twice"):
+        bat.decode_step([BatchRow(1, 0, 1), BatchRow(2, 0, 1)])
+    with pytest.raises(LokalHipError, match="exceeds"):
+        bat.decode_step([BatchRow(1, 16, 0)])
+    with pytest.raises(LokalHipError, match="exceeds"):
+        bat.decode_greedy([BatchRow(1, 10, 0)], 8)
+    with pytest.raises(LokalHipError, match="outside the vocabulary"):
+        bat.prefill(0, np.array([cfg.vocab_size], np.uint32))
+    bat.close()
+    eng.close()
+    om.close()
