@@ -238,6 +238,19 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     float* wk = wq + 64;              // [64] this token's k (the chunk holding pos)
     float* wvc = wk + 64;             // [64] this token's v
     float* wP = wvc + 64;             // [64] softmax weights of a tile, [group][jj] order
+    // The layer descriptors (weight pointers, shapes) in LDS: read from global
+    // memory mid-kernel they would be vector loads, and the s_waitcnt before
+    // the address arithmetic would also wait for every weight row already in
+    // flight (vector loads retire in order) -- a full HBM round trip per
+    // row issue.  LDS reads wait on their own counter.
+    LkFusedLayer* lay = (LkFusedLayer*)(wv + FW * 256);
+    {
+        const uint32_t* src = (const uint32_t*)a.layers;
+        uint32_t* dst = (uint32_t*)lay;
+        const uint32_t n32 = a.n_layers * (uint32_t)(sizeof(LkFusedLayer) / 4);
+        for (uint32_t i = threadIdx.x; i < n32; i += FT) dst[i] = src[i];
+        __syncthreads();
+    }
 
     Ctx c{&a, a.err, lane, wave, (int)(wave * gridDim.x + blockIdx.x), (int)(FW * gridDim.x)};
     constexpr bool KV32 = sizeof(KV) == 4;
@@ -274,11 +287,11 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         row_issue(q2, w, head * 64 + ip + 32, lane);
         const float* bias = kind == 0 ? l.bq : (kind == 1 ? l.bk : l.bv);
         if (bias) {
-            b1 = bias[head * 64 + ip];
-            b2 = bias[head * 64 + ip + 32];
+            b1 = lk_g(bias)[head * 64 + ip];
+            b2 = lk_g(bias)[head * 64 + ip + 32];
         }
     };
-    if (has1) issue_qkv(a.layers[0]);
+    if (has1) issue_qkv(lay[0]);
     // the same rotation angle every layer: pos * theta^(-2 ip / 64)
     float rc = 1.f, rsn = 0.f;
     if (has1 && kind < 2) {
@@ -295,8 +308,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
 #pragma unroll
         for (int k = 0; k < LKF_NPT; k++) {
             const uint32_t i = threadIdx.x + k * (FT / 2);
-            ngi[k] = (threadIdx.x < FT / 2 && i < h) ? l.in_norm[i] : 0.f;
-            ngp[k] = (threadIdx.x < FT / 2 && i < h) ? l.post_norm[i] : 0.f;
+            ngi[k] = (threadIdx.x < FT / 2 && i < h) ? lk_g(l.in_norm)[i] : 0.f;
+            ngp[k] = (threadIdx.x < FT / 2 && i < h) ? lk_g(l.post_norm)[i] : 0.f;
         }
     };
     auto gains_store = [&]() {
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
         }
     };
-    gains_issue(a.layers[0]);
+    gains_issue(lay[0]);
     gains_store();
 
     LKF_MARK(0);
@@ -319,7 +332,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     LKF_MARK(1);
 
     for (uint32_t L = 0; L < nL; L++) {
-        const LkFusedLayer& ly = a.layers[L];
+        const LkFusedLayer& ly = lay[L];
         const uint32_t ep = base * (nL + 1) + L + 1;
         const uint32_t par = L & 1;
         uint64_t* QB = a.qb + (size_t)par * qkvd;
@@ -621,7 +634,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
             }
             if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
-            if (has1 && L + 1 < nL) issue_qkv(a.layers[L + 1]);  // the next layer's q/k/v rows
+            if (has1 && L + 1 < nL) issue_qkv(lay[L + 1]);  // the next layer's q/k/v rows
         }
         LKF_MARK(2 + 6 * L + 4);
         // ---------------- S6: down + residual -> x of layer L+1
@@ -640,7 +653,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 if (lane == 0) publish(XN + uu, xres[uu] + d, epn);
             }
             if (L + 1 < nL) {  // read after the next stage_in's barrier
-                gains_issue(a.layers[L + 1]);
+                gains_issue(lay[L + 1]);
                 gains_store();
             }
         }
@@ -663,7 +676,8 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
     (void)max_chunks;
     uint32_t vmax = I > h ? I : h;
     if (nh * 64 > vmax) vmax = nh * 64;
-    return ((size_t)vmax + h + 16 + 2 * (size_t)h + (h & 1) + 2 * LKF_TRACE_MAX + (size_t)FW * 256) * 4;
+    return ((size_t)vmax + h + 16 + 2 * (size_t)h + (h & 1) + 2 * LKF_TRACE_MAX + (size_t)FW * 256) * 4 +
+           LK_FUSED_MAX_LAYERS * sizeof(LkFusedLayer);
 }
 int lk_fused_threads() { return FT; }
 

@@ -15,6 +15,16 @@ enum LkType : uint32_t { LK_F32 = 0, LK_F16 = 1, LK_Q8_0 = 8, LK_Q4_K = 12 };
 // src/gguf/dequant.rs:135-137).
 __device__ __forceinline__ float lk_h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
+// A pointer as a global-memory (address space 1) pointer.  Loads through a
+// generic pointer whose origin the compiler cannot see (one read from memory
+// or LDS) become flat loads, which count against lgkmcnt as well as vmcnt: every
+// later wait for an LDS read would then also wait for those loads to return
+// from HBM.  Weight, gain and bias pointers are always device allocations.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* lk_g(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+
 // Wave-64 reductions on the DPP network (no LDS round trips): quad_perm
 // pairs, row_ror 4 / 8 give every lane its 16-lane row total, row_bcast 15 /
 // 31 carry the row totals up to lane 63, whose value is broadcast.

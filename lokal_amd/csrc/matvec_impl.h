@@ -26,7 +26,7 @@ typedef unsigned int lk_u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load of weight bytes (read once per token: nontemporal).
 __device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
-    const lk_u32x4 v = __builtin_nontemporal_load((const lk_u32x4*)p);
+    const lk_u32x4 v = __builtin_nontemporal_load(lk_g((const lk_u32x4*)p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -198,8 +198,11 @@ __device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint
         const uint32_t ch0 = (uint32_t)lane + 64u * i;
         const uint32_t ch = ch0 < nchunk ? ch0 : 0u;
         R.q[i] = ld_stream16(rp + 16u * ch);
-        if constexpr (WT == LK_Q8_0) R.d[i] = (uint32_t)((const uint16_t*)ap)[ch >> 1];
-        if constexpr (WT == LK_Q4_K) R.hd[i] = *(const uint4*)(ap + 16u * (ch >> 3));
+        if constexpr (WT == LK_Q8_0) R.d[i] = (uint32_t)lk_g((const uint16_t*)ap)[ch >> 1];
+        if constexpr (WT == LK_Q4_K) {
+            const lk_u32x4 hv = *lk_g((const lk_u32x4*)(ap + 16u * (ch >> 3)));
+            R.hd[i] = make_uint4(hv.x, hv.y, hv.z, hv.w);
+        }
     }
 }
 

@@ -1,7 +1,7 @@
 """Measurements of the decode-step kernels on the workloads other than the
 headline one (bench.py measures config 3, Qwen2.5-0.5B-shape Q8_0 decode).
 
-    python -m lokal_amd.microbench [--only decode,layers,attn]
+    python -m lokal_amd.microbench [--only decode,layers,attn,gemm,prefill,batch]
 
 Prints one JSON object per measurement:
   decode  configs 1 and 4: SmolLM2-135M-shape F16 (512-token prompt, 128
@@ -13,6 +13,14 @@ Prints one JSON object per measurement:
   attn    config 5: flash-decoding of 4 sequences, one query token each, at
           contexts 4096 / 16384 / 32768 over 24 layers of f16 KV (14 q / 2 kv
           heads), µs per step and HBM GB/s of the KV bytes read once.
+  gemm    the multi-row dequant-fused GEMM (lkhip_matmul) on the Qwen2.5-0.5B
+          Q8_0 matrices for 1 / 4 / 16 / 64 / 512 activation rows: µs, weight
+          GB/s (each weight byte read once per launch) and fp32 TFLOP/s;
+  prefill config 3's 512-token prompt through Session::prefill, chunked on
+          the GEMM path and as the per-token loop (LKHIP_PREFILL=loop);
+  batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
+          with a 512-token prompt, then 64 greedy steps of all B rows on the
+          device: aggregate tok/s and weight GB/s (one weight read per step).
 Kernel times come from hipEvents around repeated launches on one stream.
 """
 from __future__ import annotations
@@ -138,9 +146,89 @@ def attn() -> list[dict]:
     return out
 
 
+def gemm() -> list[dict]:
+    """lkhip_matmul on the Qwen2.5-0.5B Q8_0 matrices."""
+    st = K.Stream()
+    out = []
+    rng = np.random.default_rng(0)
+    shapes = [("qkv", 1152, 896), ("o_proj", 896, 896), ("gate", 4864, 896), ("down", 896, 4864),
+              ("lm_head", 151936, 896)]
+    for name, rows, cols in shapes:
+        w = K.Weight(synth.Q8_0, rows, cols, synth.gen_weight(synth.Q8_0, 0, name, rows, cols).data)
+        for n in (1, 4, 16, 64, 512):
+            x = K.DeviceArray.from_numpy(rng.standard_normal((n, cols)).astype(np.float32))
+            y = K.DeviceArray((n, rows))
+            ms = _timed(lambda: K.matmul(w, x, n, y, stream=st.ptr), 20 if n < 512 else 5, st)
+            gbs = w.nbytes / (ms * 1e-3) / 1e9
+            out.append({"kernel": "gemm_q8_0", "matrix": name, "rows": rows, "cols": cols, "n_rows": n,
+                        "us": round(ms * 1e3, 2), "weight_gbs": round(gbs, 1),
+                        "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                        "tflops": round(2.0 * rows * cols * n / (ms * 1e-3) / 1e12, 2)})
+            x.free()
+            y.free()
+        w.close()
+    st.close()
+    return out
+
+
+def prefill() -> list[dict]:
+    import os
+    cfg, tensors = synth.synth_named("qwen2.5-0.5b-q8_0", 0)
+    eng = Engine.from_tensors(cfg, tensors)
+    del tensors
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab_size, 512).astype(np.uint32)
+    out = []
+    flops = 2.0 * (eng.matvec_bytes * 32 / 34) * len(prompt)  # every Q8_0 weight, every position
+    for mode in ("batched", "loop"):
+        if mode == "loop":
+            os.environ["LKHIP_PREFILL"] = "loop"
+        s = eng.session(len(prompt) + 8)
+        s.prefill(prompt[:64])  # warm-up (allocations, graph capture)
+        t0 = time.perf_counter()
+        s.prefill(prompt)
+        dt = time.perf_counter() - t0
+        s.close()
+        out.append({"workload": "qwen2.5-0.5b-q8_0 prefill", "mode": mode, "tokens": len(prompt),
+                    "ms": round(dt * 1e3, 2), "tok_s": round(len(prompt) / dt, 1),
+                    "tflops": round(flops / dt / 1e12, 2)})
+    os.environ.pop("LKHIP_PREFILL", None)
+    eng.close()
+    return out
+
+
+def batch() -> list[dict]:
+    from .engine import BatchRow
+    cfg, tensors = synth.synth_named("qwen2.5-0.5b-q8_0", 0)
+    eng = Engine.from_tensors(cfg, tensors)
+    del tensors
+    rng = np.random.default_rng(12)
+    out = []
+    steps = 64
+    for B in (1, 4, 16, 64):
+        bat = eng.batcher(B, 512 + steps + 16)
+        first = []
+        for slot in range(B):
+            lg = bat.prefill(slot, rng.integers(0, cfg.vocab_size, 512).astype(np.uint32))
+            first.append(int(np.argmax(lg)))
+        rows = [BatchRow(first[s], 512, s) for s in range(B)]
+        ids = bat.decode_greedy(rows, 8)  # warm-up: graph capture
+        rows = [BatchRow(int(ids[-1, s]), 520, s) for s in range(B)]
+        t0 = time.perf_counter()
+        bat.decode_greedy(rows, steps)
+        dt = time.perf_counter() - t0
+        bat.close()
+        tok_s = B * steps / dt
+        gbs = eng.matvec_bytes * steps / dt / 1e9
+        out.append({"workload": "qwen2.5-0.5b-q8_0 batched greedy", "rows": B, "steps": steps,
+                    "ms_per_step": round(dt / steps * 1e3, 3), "tok_s": round(tok_s, 1),
+                    "weight_gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+    eng.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", default="decode,layers,attn")
+    ap.add_argument("--only", default="decode,layers,attn,gemm,prefill,batch")
     args = ap.parse_args()
     want = set(args.only.split(","))
     if K.device_count() == 0:
@@ -155,6 +243,10 @@ def main() -> int:
     if "attn" in want:
         for r in attn():
             print(json.dumps(r), flush=True)
+    for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch)):
+        if name in want:
+            for r in fn():
+                print(json.dumps(r), flush=True)
     return 0
 
 
