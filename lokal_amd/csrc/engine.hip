@@ -493,7 +493,7 @@ enum HeadMode { HEAD_NONE = 0, HEAD_LAST = 1, HEAD_ALL = 2 };
 struct Rows {
     uint32_t cap = 0;
     DevBuf meta;   // u32 [ids | pos | slots | ctx | steps], cap each
-    DevBuf x, xn, qkv, att, inner, logits, gpart, apart, out_ids;
+    DevBuf x, xn, qkv, att, inner, logits, gpart, apart, out_ids, keys;
     size_t out_ids_cap = 0;
     uint32_t* h_meta = nullptr;  // pinned, 5 * cap
     ~Rows() {
@@ -1019,11 +1019,13 @@ static size_t rows_gemm_part(const lkhip_engine* e, uint32_t cap) {
     const lkhip_config& c = e->cfg;
     const uint32_t h = c.hidden_size, I = c.intermediate_size;
     size_t need = 0;
-    for (uint32_t n = 1; n <= cap; n++) {
-        const LkGemmPlan p[5] = {lk_gemm_plan(e->qd + 2 * e->kvd, h, n, LK_MV_STORE),
-                                 lk_gemm_plan(h, e->qd, n, LK_MV_ACC), lk_gemm_plan(I, h, n, LK_MV_SWIGLU),
-                                 lk_gemm_plan(h, I, n, LK_MV_ACC),
-                                 lk_gemm_plan(c.vocab_size, h, n < LK_ROWS_LOGITS ? n : LK_ROWS_LOGITS, LK_MV_STORE)};
+    for (uint32_t n = 1; n <= cap; n++)
+    for (const Layer& l0 : e->layers) {
+        const LkGemmPlan p[5] = {
+            lk_gemm_plan(l0.q->dw.type, e->qd + 2 * e->kvd, h, n, LK_MV_STORE),
+            lk_gemm_plan(l0.o->dw.type, h, e->qd, n, LK_MV_ACC), lk_gemm_plan(l0.gate->dw.type, I, h, n, LK_MV_SWIGLU),
+            lk_gemm_plan(l0.down->dw.type, h, I, n, LK_MV_ACC),
+            lk_gemm_plan(e->lm_head->dw.type, c.vocab_size, h, n < LK_ROWS_LOGITS ? n : LK_ROWS_LOGITS, LK_MV_STORE)};
         for (const auto& q : p) need = std::max(need, q.part_floats);
     }
     return need;
@@ -1054,6 +1056,7 @@ static int rows_alloc(const lkhip_engine* e, Rows& R, uint32_t cap, uint32_t max
         (rc = dev_alloc(R.xn, cap * h * 4)) || (rc = dev_alloc(R.qkv, cap * qkvd * 4)) ||
         (rc = dev_alloc(R.att, cap * (size_t)e->qd * 4)) || (rc = dev_alloc(R.inner, cap * I * 4)) ||
         (rc = dev_alloc(R.logits, lrows * c.vocab_size * 4)) ||
+        (rc = dev_alloc(R.keys, lrows * ((c.vocab_size + LK_ARGMAX_SLICE - 1) / LK_ARGMAX_SLICE) * 8)) ||
         (rc = dev_alloc(R.gpart, rows_gemm_part(e, cap) * 4)) ||
         (rc = dev_alloc(R.apart, lk_attn_part_floats(cap, c.num_attention_heads, max_seq) * 4)))
         return rc;
@@ -1084,9 +1087,16 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
         if ((err = (call)) != hipSuccess) return err; \
     } while (0)
     RSTEP(lk_gather_launch(e->embed->dw, ids, n, x, st));
+    // Split-K partials of the QKV, o_proj and down GEMMs are summed by the
+    // kernel that consumes them (RoPE + KV append, residual add + RMSNorm)
+    // rather than by a reduce launch of their own.
+    float* part = R.gpart.as<float>();
+    uint32_t pend = 0;  // down partials of the previous layer not yet added to x
     for (uint32_t L = 0; L < c.num_hidden_layers; L++) {
         const Layer& ly = e->layers[L];
-        RSTEP(lk_rmsnorm_launch(x, ly.in_norm.as<float>(), n, h, c.rms_norm_eps, xn, st));
+        if (L == 0) RSTEP(lk_rmsnorm_launch(x, ly.in_norm.as<float>(), n, h, c.rms_norm_eps, xn, st));
+        else RSTEP(lk_rows_accnorm_launch(x, part, pend, n, h, ly.in_norm.as<float>(), c.rms_norm_eps, xn, st));
+        uint32_t ks = 0;
         {
             LkGemmArgs a{};
             a.nseg = 3;
@@ -1099,12 +1109,18 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.x = xn;
             a.ldx = h;
             a.ldy = qkvd;
-            RSTEP(rows_gemm(R, a, LK_MV_STORE, st));
+            a.part = part;
+            RSTEP(lk_gemm_launch(a, LK_MV_STORE, st, &ks));
         }
         uint8_t* kc = kv.kc + L * kv.layer_bytes;
         uint8_t* vc = kv.vc + L * kv.layer_bytes;
-        RSTEP(lk_rope_kv_launch(qkv, c.num_attention_heads, c.num_key_value_heads, e->freq, nullptr, pos, n, kc, vc,
-                                kv.kv_f32, kv.kv_seq, kv.slot_elems, slots, st));
+        RSTEP(lk_rows_rope_kv_launch(qkv, part, ks, ly.has_bias ? ly.bq.as<float>() : nullptr,
+                                     ly.has_bias ? ly.bk.as<float>() : nullptr,
+                                     ly.has_bias ? ly.bv.as<float>() : nullptr, c.num_attention_heads,
+                                     c.num_key_value_heads, e->freq, pos, n, kc, vc, kv.kv_f32, kv.kv_seq,
+                                     kv.slot_elems, slots, st));
+        // without logits only the last layer's K/V are needed from it
+        if (head == HEAD_NONE && L + 1 == c.num_hidden_layers) break;
         {
             LkAttnArgs a{};
             a.q = qkv;
@@ -1133,9 +1149,10 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.x = att;
             a.ldx = qd;
             a.ldy = h;
-            RSTEP(rows_gemm(R, a, LK_MV_ACC, st));
+            a.part = part;
+            RSTEP(lk_gemm_launch(a, LK_MV_ACC, st, &ks));
         }
-        RSTEP(lk_rmsnorm_launch(x, ly.post_norm.as<float>(), n, h, c.rms_norm_eps, xn, st));
+        RSTEP(lk_rows_accnorm_launch(x, part, ks, n, h, ly.post_norm.as<float>(), c.rms_norm_eps, xn, st));
         {
             LkGemmArgs a{};
             a.nseg = 2;
@@ -1159,20 +1176,20 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.x = inner;
             a.ldx = I;
             a.ldy = h;
-            RSTEP(rows_gemm(R, a, LK_MV_ACC, st));
+            a.part = part;
+            RSTEP(lk_gemm_launch(a, LK_MV_ACC, st, &pend));
         }
     }
     if (head != HEAD_NONE) {
         const uint32_t hr = head == HEAD_ALL ? n : 1;
-        const float* xs = head == HEAD_ALL ? x : x + (size_t)(n - 1) * h;
-        RSTEP(lk_rmsnorm_launch(xs, e->norm.as<float>(), hr, h, c.rms_norm_eps, xn, st));
+        RSTEP(lk_rows_accnorm_launch(x, part, pend, n, h, e->norm.as<float>(), c.rms_norm_eps, xn, st));
         LkGemmArgs a{};
         a.nseg = 1;
         a.seg[0] = {e->lm_head->dw, nullptr, R.logits.as<float>()};
         a.N = c.vocab_size;
         a.K = h;
         a.n_rows = hr;
-        a.x = xn;
+        a.x = head == HEAD_ALL ? xn : xn + (size_t)(n - 1) * h;
         a.ldx = h;
         a.ldy = c.vocab_size;
         RSTEP(rows_gemm(R, a, LK_MV_STORE, st));
@@ -1346,8 +1363,8 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy) {
     auto body = [&](hipStream_t st) -> hipError_t {
         hipError_t err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;
-        return lk_rows_greedy_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.meta.as<uint32_t>(),
-                                     b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
+        return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
+                                      b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
     };
     if (!graphs_on()) {
         hipError_t err = body(b->stream);
@@ -1606,7 +1623,7 @@ extern "C" int lkhip_matmul(const lkhip_weight* w, const float* x, size_t n_rows
     if (ldx < d.cols || ldy < d.rows || ldx % 4 || (uintptr_t)x % 16)
         return fail(LKHIP_E_INVALID, "matmul: ldx must be >= cols and a multiple of 4, x 16-byte aligned, ldy >= rows");
     const int mode = accumulate ? LK_MV_ACC : LK_MV_STORE;
-    const LkGemmPlan p = lk_gemm_plan(d.rows, d.cols, (uint32_t)n_rows, mode);
+    const LkGemmPlan p = lk_gemm_plan(d.type, d.rows, d.cols, (uint32_t)n_rows, mode);
     hipStream_t st = (hipStream_t)stream;
     void* part = nullptr;
     if (p.part_floats) HIP_OR_FAIL(hipMallocAsync(&part, p.part_floats * 4, st));

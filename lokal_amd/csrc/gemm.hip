@@ -312,7 +312,8 @@ hipError_t launch_t(const LkGemmArgs& a, int mode, uint32_t mb, dim3 grid, hipSt
 
 static uint32_t gemm_mb(uint32_t n_rows) { return n_rows <= 16 ? 1 : 2; }
 
-LkGemmPlan lk_gemm_plan(uint32_t N, uint32_t K, uint32_t n_rows, int mode) {
+LkGemmPlan lk_gemm_plan(uint32_t type, uint32_t N, uint32_t K, uint32_t n_rows, int mode) {
+    (void)type;
     LkGemmPlan p{};
     p.mb = gemm_mb(n_rows);
     const uint32_t gx = (N + 63) / 64, gy = (n_rows + 16 * p.mb - 1) / (16 * p.mb);
@@ -333,7 +334,7 @@ bool lk_gemm_shape_ok(uint32_t type, uint32_t N, uint32_t K) {
     return type == LK_Q8_0 || type == LK_F16 || type == LK_Q4_K;
 }
 
-hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st) {
+hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st, uint32_t* deferred_ks) {
     const uint32_t type = a.seg[0].w.type;
     if (a.n_rows == 0) return hipSuccess;
     if (!lk_gemm_shape_ok(type, a.N, a.K) || (mode != LK_MV_STORE && mode != LK_MV_ACC && mode != LK_MV_SWIGLU))
@@ -345,7 +346,7 @@ hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st) {
         for (uint32_t i = 0; i + 1 < a.nseg; i++)
             if (a.seg[i].w.rows % 16) return hipErrorInvalidValue;
     if (a.ldx % 4 || (size_t)(uintptr_t)a.x % 16) return hipErrorInvalidValue;  // float4 X loads
-    const LkGemmPlan p = lk_gemm_plan(a.N, a.K, a.n_rows, mode);
+    const LkGemmPlan p = lk_gemm_plan(type, a.N, a.K, a.n_rows, mode);
     if (a.ks == 0) a.ks = p.ks;
     if (a.ks > 1 && !a.part) return hipErrorInvalidValue;
     dim3 grid((a.N + 63) / 64, (a.n_rows + 16 * p.mb - 1) / (16 * p.mb), a.ks);
@@ -355,7 +356,8 @@ hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st) {
     case LK_F16: e = lkg::launch_t<LK_F16>(a, mode, p.mb, grid, st); break;
     default: e = lkg::launch_t<LK_Q4_K>(a, mode, p.mb, grid, st); break;
     }
-    if (e != hipSuccess || a.ks == 1) return e;
+    if (deferred_ks) *deferred_ks = a.ks > 1 ? a.ks : 0;
+    if (e != hipSuccess || a.ks == 1 || deferred_ks) return e;
     hipLaunchKernelGGL(lkg::gemm_reduce_kernel, dim3((a.N + 255) / 256, a.n_rows), dim3(256), 0, st, a, mode);
     return hipGetLastError();
 }

@@ -214,22 +214,146 @@ hipError_t lk_step_finish_launch(const uint64_t* keys, uint32_t n_keys, LkStepSt
     return hipGetLastError();
 }
 
-// Greedy step of a batch of sequences (generate.rs:101-118 at -t 0, one row
-// per sequence): row r's argmax (src/sampler.rs:67-75, first max wins) is
-// recorded as that row's next output id and fed back as its next token at the
-// next position.  meta holds u32 arrays [ids | pos | slots | ctx | steps],
-// each `cap` long; out_ids is [step][n_rows].
-__global__ __launch_bounds__(1024) void rows_greedy_kernel(const float* __restrict__ logits, uint32_t n,
-                                                           uint32_t* __restrict__ meta, uint32_t cap,
-                                                           uint32_t n_rows, uint32_t* __restrict__ out_ids) {
+// ------------------------------------------------ rows-path fused consumers
+// The residual add of a split-K GEMM's partials (src/model.rs:235-237,
+// :253-255; summed in split order, as gemm_reduce_kernel would) fused with the
+// RMSNorm that reads the new residual (src/math.rs:45-49).  One block per row.
+__global__ __launch_bounds__(1024) void rows_accnorm_kernel(float* __restrict__ x, const float* __restrict__ part,
+                                                            uint32_t ks, uint32_t rows, uint32_t n,
+                                                            const float* __restrict__ w, float eps,
+                                                            float* __restrict__ y) {
+    // 1024 threads: one element each at the model widths, so a thread's ks
+    // partial loads are all in flight together
     const uint32_t r = blockIdx.x;
-    const float* xr = logits + (size_t)r * n;
+    float* xr = x + (size_t)r * n;
+    __shared__ float red[16];
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        float v = xr[i];
+        if (ks) {
+            float a = 0.f;
+#pragma unroll 8
+            for (uint32_t z = 0; z < ks; z++) a += part[((size_t)z * rows + r) * n + i];
+            v += a;
+            xr[i] = v;
+        }
+        ss = fmaf(v, v, ss);
+    }
+    ss = lk_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) tot += red[i];
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) y[(size_t)r * n + i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+}
+
+hipError_t lk_rows_accnorm_launch(float* x, const float* part, uint32_t ks, uint32_t rows, uint32_t n,
+                                  const float* w, float eps, float* y, hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rows_accnorm_kernel, dim3(rows), dim3(1024), 0, st, x, part, ks, rows, n, w, eps, y);
+    return hipGetLastError();
+}
+
+// The QKV split-K sum (+ q/k/v bias, src/model.rs:27-35) fused with RoPE and
+// the KV append of rope_kv_kernel.
+template <typename KV>
+__global__ __launch_bounds__(256) void rows_rope_kv_kernel(float* __restrict__ qkv, const float* __restrict__ part,
+                                                           uint32_t ks, const float* __restrict__ bq,
+                                                           const float* __restrict__ bk,
+                                                           const float* __restrict__ bv, uint32_t n_heads,
+                                                           uint32_t n_kv, const LkFreq fr,
+                                                           const uint32_t* __restrict__ pos_rows, uint32_t rows,
+                                                           KV* __restrict__ kc, KV* __restrict__ vc,
+                                                           uint32_t max_seq, uint64_t slot_stride,
+                                                           const uint32_t* __restrict__ slots) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t pos = pos_rows[r];
+    const uint32_t slot = slots[r];
+    const uint32_t qd = n_heads * 64, kvd = n_kv * 64, qkvd = qd + 2 * kvd;
+    float* row = qkv + (size_t)r * qkvd;
+    auto val = [&](uint32_t idx) -> float {
+        if (!ks) return row[idx];
+        float a = 0.f;
+        for (uint32_t z = 0; z < ks; z++) a += part[((size_t)z * rows + r) * qkvd + idx];
+        const float* b = idx < qd ? bq : (idx < qd + kvd ? bk : bv);
+        const uint32_t bi = idx < qd ? idx : (idx < qd + kvd ? idx - qd : idx - qd - kvd);
+        return b ? a + b[bi] : a;
+    };
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t nq_pairs = n_heads * 32, nk_pairs = n_kv * 32;
+    const float fpos = (float)pos;
+    if (t < nq_pairs) {
+        const uint32_t head = t / 32, i = t % 32;
+        const uint32_t o = head * 64 + i;
+        float a = val(o), b = val(o + 32);
+        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        row[o] = a;
+        row[o + 32] = b;
+    } else if (t < nq_pairs + nk_pairs) {
+        const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
+        const uint32_t o = qd + head * 64 + i;
+        float a = val(o), b = val(o + 32);
+        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
+        kv_store(dst + i, a);
+        kv_store(dst + i + 32, b);
+    } else if (t < nq_pairs + nk_pairs + kvd) {
+        const uint32_t u = t - nq_pairs - nk_pairs, head = u / 64, d = u % 64;
+        kv_store(vc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d, val(qd + kvd + u));
+    }
+}
+
+hipError_t lk_rows_rope_kv_launch(float* qkv, const float* part, uint32_t ks, const float* bq, const float* bk,
+                                  const float* bv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
+                                  const uint32_t* pos_rows, uint32_t n_rows, void* kcache, void* vcache, int kv_f32,
+                                  uint32_t max_seq, uint64_t slot_stride, const uint32_t* slots, hipStream_t st) {
+    if (n_rows == 0) return hipSuccess;
+    const uint32_t work = n_heads * 32 + n_kv * 32 + n_kv * 64;
+    dim3 grid((work + 255) / 256, n_rows);
+    if (kv_f32)
+        hipLaunchKernelGGL(rows_rope_kv_kernel<float>, grid, dim3(256), 0, st, qkv, part, ks, bq, bk, bv, n_heads,
+                           n_kv, freq, pos_rows, n_rows, (float*)kcache, (float*)vcache, max_seq, slot_stride, slots);
+    else
+        hipLaunchKernelGGL(rows_rope_kv_kernel<uint16_t>, grid, dim3(256), 0, st, qkv, part, ks, bq, bk, bv, n_heads,
+                           n_kv, freq, pos_rows, n_rows, (uint16_t*)kcache, (uint16_t*)vcache, max_seq, slot_stride,
+                           slots);
+    return hipGetLastError();
+}
+
+// Greedy step of a batch of sequences (generate.rs:101-118 at -t 0, one row
+// per sequence) in two passes: every block takes the first-max key
+// (src/sampler.rs:67-75) of one LK_ARGMAX_SLICE-wide slice of one row, then
+// one wave per row folds the slice keys, records the winner as the row's next
+// output id (out_ids is [step][n_rows]) and feeds it back as the row's next
+// token at the next position.  meta holds u32 arrays
+// [ids | pos | slots | ctx | steps], each `cap` long.
+__global__ __launch_bounds__(256) void argmax_slices_kernel(const float* __restrict__ x, uint32_t n,
+                                                            uint64_t* __restrict__ keys) {
+    const uint32_t r = blockIdx.y, sl = blockIdx.x, ns = gridDim.x;
+    const float* xr = x + (size_t)r * n;
+    const uint32_t i0 = sl * LK_ARGMAX_SLICE, i1 = i0 + LK_ARGMAX_SLICE < n ? i0 + LK_ARGMAX_SLICE : n;
     uint64_t k = 0;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    for (uint32_t i = i0 + threadIdx.x; i < i1; i += 256) {
         const uint64_t kk = lk_argmax_key(xr[i], i);
         k = kk > k ? kk : k;
     }
     k = max_key_block(k);
+    if (threadIdx.x == 0) keys[(size_t)r * ns + sl] = k;
+}
+
+__global__ __launch_bounds__(64) void rows_fold_kernel(const uint64_t* __restrict__ keys, uint32_t ns,
+                                                       uint32_t* __restrict__ meta, uint32_t cap, uint32_t n_rows,
+                                                       uint32_t* __restrict__ out_ids) {
+    const uint32_t r = blockIdx.x;
+    uint64_t k = 0;
+    for (uint32_t i = threadIdx.x; i < ns; i += 64) k = keys[(size_t)r * ns + i] > k ? keys[(size_t)r * ns + i] : k;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
     if (threadIdx.x == 0) {
         const uint32_t id = lk_argmax_idx(k);
         uint32_t* ids = meta;
@@ -244,9 +368,11 @@ __global__ __launch_bounds__(1024) void rows_greedy_kernel(const float* __restri
     }
 }
 
-hipError_t lk_rows_greedy_launch(const float* logits, uint32_t n_rows, uint32_t n, uint32_t* meta, uint32_t cap,
-                                 uint32_t* out_ids, hipStream_t st) {
+hipError_t lk_rows_greedy2_launch(const float* logits, uint32_t n_rows, uint32_t n, uint64_t* keys, uint32_t* meta,
+                                  uint32_t cap, uint32_t* out_ids, hipStream_t st) {
     if (n_rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(rows_greedy_kernel, dim3(n_rows), dim3(1024), 0, st, logits, n, meta, cap, n_rows, out_ids);
+    const uint32_t ns = (n + LK_ARGMAX_SLICE - 1) / LK_ARGMAX_SLICE;
+    hipLaunchKernelGGL(argmax_slices_kernel, dim3(ns, n_rows), dim3(256), 0, st, logits, n, keys);
+    hipLaunchKernelGGL(rows_fold_kernel, dim3(n_rows), dim3(64), 0, st, keys, ns, meta, cap, n_rows, out_ids);
     return hipGetLastError();
 }

@@ -212,14 +212,27 @@ struct LkGemmArgs {
 // Plan: K splits for a launch and the partial floats it needs.
 struct LkGemmPlan {
     uint32_t ks;
-    uint32_t mb;       // 16-row batch tiles per wave (1, 2 or 4)
+    uint32_t mb;       // 16-row batch tiles per wave (1 or 2)
     size_t part_floats;
 };
-LkGemmPlan lk_gemm_plan(uint32_t N, uint32_t K, uint32_t n_rows, int mode);
+LkGemmPlan lk_gemm_plan(uint32_t type, uint32_t N, uint32_t K, uint32_t n_rows, int mode);
 // Checks the shape the GEMM assumes: N a multiple of 16 per segment, K of 32.
 bool lk_gemm_shape_ok(uint32_t type, uint32_t N, uint32_t K);
-hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st);
-// Batched greedy step (layer.hip): argmax of each logits row fed back into the
-// row's token / position (meta = [ids | pos | slots | ctx | steps], cap each).
-hipError_t lk_rows_greedy_launch(const float* logits, uint32_t n_rows, uint32_t n, uint32_t* meta, uint32_t cap,
-                                 uint32_t* out_ids, hipStream_t st);
+// deferred_ks != null: a split launch leaves its partials [ks][n_rows][N] in
+// a.part for the consumer to sum (*deferred_ks = ks, 0 when not split, in
+// which case the epilogue already ran); the consumer applies bias / residual.
+hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st, uint32_t* deferred_ks = nullptr);
+// Rows-path consumers of deferred split-K partials (layer.hip):
+//  x[r] += sum_z part[z][r] (ks > 0), then y[r] = rmsnorm(x[r]) * w
+hipError_t lk_rows_accnorm_launch(float* x, const float* part, uint32_t ks, uint32_t rows, uint32_t n,
+                                  const float* w, float eps, float* y, hipStream_t st);
+//  qkv[r] = sum_z part[z][r] + bias (ks > 0), then the rope_kv work of
+//  lk_rope_kv_launch (rotated q back into qkv, k/v into the cache)
+hipError_t lk_rows_rope_kv_launch(float* qkv, const float* part, uint32_t ks, const float* bq, const float* bk,
+                                  const float* bv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
+                                  const uint32_t* pos_rows, uint32_t n_rows, void* kcache, void* vcache, int kv_f32,
+                                  uint32_t max_seq, uint64_t slot_stride, const uint32_t* slots, hipStream_t st);
+//  greedy step of every row in two passes: per-slice argmax keys, then fold
+hipError_t lk_rows_greedy2_launch(const float* logits, uint32_t n_rows, uint32_t n, uint64_t* keys, uint32_t* meta,
+                                  uint32_t cap, uint32_t* out_ids, hipStream_t st);
+#define LK_ARGMAX_SLICE 4096u
