@@ -200,7 +200,10 @@ def main() -> int:
             "algorithmic_bytes_per_token": mv_bytes,
             "profiled_tokens": int(prof["tokens"]),
         },
-        "prefill_s": round(prefill_s, 3),
+        # untimed context: the 512-token prompt through Session::prefill (one
+        # chunk on the multi-row GEMM path; includes its first-use allocation)
+        "prefill": {"tokens": args.prompt, "s": round(prefill_s, 4),
+                    "tok_s": round(args.prompt / prefill_s, 1)},
     }
     sess.close()
     eng.close()
