@@ -42,11 +42,11 @@ struct LkFusedArgs {
 };
 // ... followed by 8 sub-steps of layer 1's attention stage (when the traced
 // block runs an attention unit there).
-__host__ __device__ inline uint32_t lk_fused_trace_len(uint32_t n_layers) { return 2 + 6 * n_layers + 1 + 16; }
+__host__ __device__ inline uint32_t lk_fused_trace_len(uint32_t n_layers) { return 2 + 6 * n_layers + 1 + 24; }
 // Shape limits of the one-kernel step: hidden width (RMSNorm gains held by
 // 4 per thread) and layers (stage timestamps kept in 256 LDS slots).
 #define LK_FUSED_MAX_H 2048u
-#define LK_FUSED_MAX_LAYERS 39u
+#define LK_FUSED_MAX_LAYERS 38u
 
 // LDS of one workgroup for sessions of up to max_chunks 64-position tiles.
 size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks);

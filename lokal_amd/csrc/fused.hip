@@ -98,7 +98,9 @@ __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
 }
 
 // Words src[i0 + k*step], k < N, i < n, into dst[...]: all N loads are in
-// flight together; only words not yet carrying the epoch are polled again.
+// flight together, and every round re-polls all the words still missing
+// together, so a late vector costs one round trip per round rather than one
+// per missing word.  Bounded like await().
 template <int N>
 __device__ __forceinline__ void awaitN(const Ctx& c, const uint64_t* src, uint32_t i0, uint32_t step, uint32_t n,
                                        uint32_t ep, float* dst) {
@@ -106,12 +108,29 @@ __device__ __forceinline__ void awaitN(const Ctx& c, const uint64_t* src, uint32
 #pragma unroll
     for (int k = 0; k < N; k++) {
         const uint32_t i = i0 + k * step;
-        w[k] = i < n ? ld_word(src + i) : 0;
+        w[k] = i < n ? ld_word(src + i) : ((uint64_t)ep << 32);
+    }
+    for (uint32_t r = 0;; r++) {
+        bool done = true;
+#pragma unroll
+        for (int k = 0; k < N; k++) done &= (uint32_t)(w[k] >> 32) == ep;
+        if (done) break;
+        if ((r & 255) == 255) {
+            if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+            if (r > (1u << 21)) {
+                __hip_atomic_store(c.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if ((uint32_t)(w[k] >> 32) != ep) w[k] = ld_word(src + i0 + k * step);
     }
 #pragma unroll
     for (int k = 0; k < N; k++) {
         const uint32_t i = i0 + k * step;
-        if (i < n) dst[i] = (uint32_t)(w[k] >> 32) == ep ? __uint_as_float((uint32_t)w[k]) : await(c, src + i, ep);
+        if (i < n) dst[i] = __uint_as_float((uint32_t)w[k]);
     }
 }
 
@@ -280,25 +299,24 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     if (tracing && threadIdx.x == 0)
         for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) ltr[k] = 0;
     Row<WT, NCHH> q1, q2;  // prefetched one stage ahead (layer L's rows during layer L-1's down)
-    float b1 = 0.f, b2 = 0.f;  // their biases
     auto issue_qkv = [&](const LkFusedLayer& l) {
         const LkDevW& w = kind == 0 ? l.q : (kind == 1 ? l.k : l.v);
         row_issue(q1, w, head * 64 + ip, lane);
         row_issue(q2, w, head * 64 + ip + 32, lane);
-        const float* bias = kind == 0 ? l.bq : (kind == 1 ? l.bk : l.bv);
-        if (bias) {
-            b1 = lk_g(bias)[head * 64 + ip];
-            b2 = lk_g(bias)[head * 64 + ip + 32];
-        }
     };
     if (has1) issue_qkv(lay[0]);
-    // the same rotation angle every layer: pos * theta^(-2 ip / 64)
+    // the same rotation angle every layer: pos * theta^(-2 ip / 64).  It is
+    // wave-uniform, so it lives in scalar registers: a value the register
+    // allocator spills to scratch is reloaded with a vector-memory wait that
+    // also waits for every weight row in flight.
     float rc = 1.f, rsn = 0.f;
     if (has1 && kind < 2) {
         const float ang = __fmul_rn(fpos, a.freq.f[ip]);
         rsn = sinf(ang);
         rc = cosf(ang);
     }
+    rc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rc)));
+    rsn = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rsn)));
     // a layer's RMSNorm gains go to LDS one layer ahead (loaded into
     // registers during the previous layer's down stage)
     // (loaded by half 0 only: half 1 polls first in the next layer)
@@ -359,11 +377,24 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         Row<WT, NCHH> gq[LKF_KB], uq[LKF_KB];  // issued in S1 (half 1) or S4 (half 0), used in S5
         Row<WT, NCHI> dn;                   // issued in S5, used in S6
         // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
+        // biases load while the input vector is awaited (held across stages
+        // they would be spilled, see rc above)
+        float b1 = 0.f, b2 = 0.f;
+        if (has1) {
+            const float* bias = kind == 0 ? ly.bq : (kind == 1 ? ly.bk : ly.bv);
+            if (bias) {
+                b1 = lk_g(bias)[head * 64 + ip];
+                b2 = lk_g(bias)[head * 64 + ip + 32];
+            }
+        }
         if (L > 0) stage_in<8>(c, a.xb + (size_t)par * h, h, ep, xres, 1);
+        LKF_SUB(15);
         rmsnorm_lds(xres, gin, h, a.eps, xin, red);
+        LKF_SUB(16);
         if (has1) {
             float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
             float d2 = lk_wave_sum(row_dot(q2, xin, h, lane));
+            LKF_SUB(17);
             if (lane == 0) {
                 const uint32_t r = head * 64 + ip;
                 d1 += b1;  // zero when the model has no q/k/v biases
@@ -383,6 +414,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
             }
         }
+        LKF_SUB(18);
         if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
         if (half1) {
 #pragma unroll
@@ -642,8 +674,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             const uint32_t epn = ep + 1;
             uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * h;
             stage_in<24>(c, IB, I, ep, xin, 1);
+            LKF_SUB(7);
             if (c.gw < (int)h) {
                 const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
+                LKF_SUB(19);
                 if (lane == 0) publish(XN + c.gw, xres[c.gw] + d, epn);
             }
             for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {

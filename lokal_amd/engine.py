@@ -185,10 +185,10 @@ class Session:
         """Stage durations (us) of the last one-kernel step, for the traced block
         (the final norm + lm_head + argmax is a separate launch, not traced)."""
         L = self.engine.cfg.num_hidden_layers
-        n = 2 + 6 * L + 1 + 16  # stage marks, end of block, then sub-steps of layer 1
+        n = 2 + 6 * L + 1 + 24  # stage marks, end of block, then sub-steps of layer 1
         t = np.zeros(n, dtype=np.uint64)
         check(lib().lkhip_session_trace(self._h, t.ctypes.data_as(C.POINTER(C.c_uint64)), n))
-        t = t[:n - 16]
+        t = t[:n - 24]
         us = np.diff(t.astype(np.float64)) / 100.0  # 100 MHz counter
         names = ["qkv", "attn", "merge", "o_proj", "gate_up", "down"]
         per = us[1:1 + 6 * L].reshape(L, 6)
