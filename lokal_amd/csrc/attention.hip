@@ -18,6 +18,9 @@
 // max-rescaled sums.  fp32 throughout; scale 1/sqrt(64) = 0.125 is exact.
 #include "lkhip_common.h"
 
+#include <cstdlib>
+#include <cstring>
+
 #define LK_HD 64
 #define LK_ACHUNK 256
 
@@ -194,6 +197,196 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     }
 }
 
+// The f16-cache partial on the matrix cores.  Same block/tile split as
+// attn_partial_kernel (a 256-position chunk per block, a 64-position tile per
+// wave), with both products on v_mfma_f32_16x16x16f16:
+//   scores : S[pos][head] = K . q, 16 positions x 16 heads (G used) per MFMA,
+//            K rows exact in f16, q split into f16 hi + lo (22 significant
+//            bits), f32 accumulation.  Lane l holds row pos0 + (l & 15) of K
+//            and dims 16*(l >> 4) .. +15 -- the same dims for q -- so a wave's
+//            K load is 16 whole 128-byte rows;
+//   softmax: per head (lane & 15) over the wave's 64 positions;
+//   P.V    : O[head][dim] = P . V with P straight from the score registers
+//            (lane l holds P[head l & 15][positions 4*(l >> 4) .. +3], exactly
+//            the A-operand layout), split hi + lo like q, and V read back from
+//            LDS in the B-operand layout (the tile is staged there by
+//            coalesced 16-byte loads).
+// At GQA 7 this is ~1/5 of the vector-ALU work of the scalar kernel, whose
+// FMA rate per HBM byte is close to the ALU's.
+typedef _Float16 lk_h4 __attribute__((ext_vector_type(4)));
+typedef float lk_f4 __attribute__((ext_vector_type(4)));
+#define LK_VS 72  // LDS row stride of a staged V tile (halves)
+
+__device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
+    const uint2 u = make_uint2(lo, hi);
+    return __builtin_bit_cast(lk_h4, u);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
+    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const uint32_t ctx = attn_ctx(a, seq);
+    const uint32_t c0 = chunk * LK_ACHUNK;
+    if (c0 >= ctx) return;  // uniform over the block
+    const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
+    const uint32_t slot = a.slots ? a.slots[seq] : seq;
+    const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
+    const uint16_t* __restrict__ K = (const uint16_t*)a.k + kv_base;
+    const uint16_t* __restrict__ V = (const uint16_t*)a.v + kv_base;
+
+    // the staged V tiles, reused for the waves' O tiles once all P.V are done
+    __shared__ __align__(16) uint16_t vs[4][64 * LK_VS];
+    __shared__ float red_m[4][16], red_l[4][16];
+    float(*red_acc)[16][LK_HD] = (float(*)[16][LK_HD])&vs[0][0];
+    static_assert(sizeof(vs) >= 4 * 16 * LK_HD * sizeof(float), "O tiles fit the V staging area");
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t j = (uint32_t)lane >> 4, c16 = (uint32_t)lane & 15;
+    const uint32_t p0 = c0 + (uint32_t)w * 64;
+    const bool tile_live = p0 < ctx;  // wave-uniform
+    const uint32_t plast = ctx - 1;
+
+    // K: sub-tile t rows p0 + 16t + c16, this lane's 32 bytes (dims 16j..16j+15);
+    // V: rows p0 + 8it + (lane >> 3), bytes 16*(lane & 7) -- 1 KiB per instruction
+    uint4 kr[4][2], vr[8];
+    if (tile_live) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t p = p0 + 16u * t + c16;
+            const uint4* src = (const uint4*)(K + (size_t)(p < ctx ? p : plast) * LK_HD + 16 * j);
+            kr[t][0] = src[0];
+            kr[t][1] = src[1];
+        }
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const uint32_t p = p0 + 8u * it + ((uint32_t)lane >> 3);
+            vr[it] = *(const uint4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
+        }
+    }
+    // q of head c16 (zero past G), dims 16j + 4s .. +3 for step s, as f16 hi + lo
+    lk_h4 qh[4], ql[4];
+    {
+        const float* qrow = a.q + (size_t)seq * a.q_stride + ((size_t)kvh * G + (c16 < (uint32_t)G ? c16 : 0)) * LK_HD;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const float4 v = *(const float4*)(qrow + 16 * j + 4 * st);
+            const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float xv = c16 < (uint32_t)G ? x[e] : 0.f;
+                const _Float16 hi = (_Float16)xv;
+                qh[st][e] = hi;
+                ql[st][e] = (_Float16)(xv - (float)hi);
+            }
+        }
+    }
+    float mt = -INFINITY, lt = 0.f;
+    lk_f4 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) o[d] = lk_f4{0.f, 0.f, 0.f, 0.f};
+    if (tile_live) {
+        uint16_t* vw = vs[w];
+#pragma unroll
+        for (int it = 0; it < 8; it++)
+            *(uint4*)&vw[(8 * it + (lane >> 3)) * LK_VS + 8 * (lane & 7)] = vr[it];
+        // ---- scores
+        lk_f4 sc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lk_f4 acc = lk_f4{0.f, 0.f, 0.f, 0.f};
+            const uint32_t kw[8] = {kr[t][0].x, kr[t][0].y, kr[t][0].z, kr[t][0].w,
+                                    kr[t][1].x, kr[t][1].y, kr[t][1].z, kr[t][1].w};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const lk_h4 kk = h4_bits(kw[2 * st], kw[2 * st + 1]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qh[st], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, ql[st], acc, 0, 0, 0);
+            }
+            sc[t] = acc;  // lane: positions p0 + 16t + 4j + i, head c16
+        }
+        // ---- softmax over the wave's 64 positions, per head (lanes c16, +16, +32, +48)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t p = p0 + 16u * t + 4u * j + (uint32_t)i;
+                const float v = p < ctx ? sc[t][i] * 0.125f : -INFINITY;
+                sc[t][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float sum = 0.f;
+        lk_h4 ph[4], pl[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float pe = expf(sc[t][i] - mx);  // 0 for masked positions
+                sum += pe;
+                const _Float16 hi = (_Float16)pe;
+                ph[t][i] = hi;
+                pl[t][i] = (_Float16)(pe - (float)hi);
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        mt = mx;
+        lt = sum;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the V tile is in LDS
+        __builtin_amdgcn_wave_barrier();
+        // ---- P.V: k = positions 16t + 4j + i, n = dims 16d + c16
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint16_t* vp = &vw[(16 * t + 4 * j) * LK_VS + 16 * d + c16];
+                const uint32_t v01 = (uint32_t)vp[0] | ((uint32_t)vp[LK_VS] << 16);
+                const uint32_t v23 = (uint32_t)vp[2 * LK_VS] | ((uint32_t)vp[3 * LK_VS] << 16);
+                const lk_h4 vb = h4_bits(v01, v23);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[t], vb, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[t], vb, o[d], 0, 0, 0);
+            }
+        }
+    }
+    // o[d] lane: heads 4j + i, dim 16d + c16 (relative to this wave's max)
+    __syncthreads();  // every wave is done with its V tile
+    if (j == 0) {
+        red_m[w][c16] = mt;  // -inf for a wave with no live tile
+        red_l[w][c16] = lt;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][16 * d + c16] = o[d][i];
+    __syncthreads();
+
+    // ---- merge the 4 tiles into one partial per query head
+    float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * max_chunks + chunk) * (2 + LK_HD);
+    for (int t = tid; t < G * LK_HD; t += 256) {
+        const int g = t / LK_HD, dd = t % LK_HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, red_m[ww][g]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            if (red_m[ww][g] != -INFINITY) {
+                const float scl = expf(red_m[ww][g] - M);
+                L = fmaf(scl, red_l[ww][g], L);
+                A = fmaf(scl, red_acc[ww][g][dd], A);
+            }
+        }
+        float* ph = part + (size_t)g * max_chunks * (2 + LK_HD);
+        if (dd == 0) {
+            ph[0] = M;
+            ph[1] = L;
+        }
+        ph[2 + dd] = A;
+    }
+}
+
 // Fold the chunk partials of one query head: out = sum_c e^{m_c-M} acc_c /
 // sum_c e^{m_c-M} l_c.  Four waves take interleaved quarters of the chunks
 // (lane = dim; 16 chunks' words in flight per lane), each folding online
@@ -261,9 +454,16 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
     const uint32_t G = a.n_heads / a.n_kv;
     const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     dim3 grid(max_chunks, a.n_kv, a.n_seq);
+    // The matrix-core kernel is faster up to ~8k positions (4 sequences x 24
+    // layers at ctx 4096: 8.7 vs 10.6 us per launch) and slower beyond (ctx
+    // 32768: 28.4 vs 21.7 us); LKHIP_ATTN=valu / =mfma force one of them.
+    const char* fe = getenv("LKHIP_ATTN");
+    const int force = fe ? (strcmp(fe, "valu") == 0 ? 1 : (strcmp(fe, "mfma") == 0 ? 2 : 0)) : 0;
+    const bool mfma = force == 2 || (force == 0 && a.max_seq <= 8192);
 #define LK_ATTN_CASE(g)                                                                         \
     case g:                                                                                     \
         if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(256), 0, st, a); \
+        else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g>), grid, dim3(256), 0, st, a);     \
         else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(256), 0, st, a);  \
         break;
     switch (G) {

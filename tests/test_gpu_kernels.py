@@ -231,6 +231,17 @@ def test_attention_config5_four_sequences_32k():
     _attn_case(4, 14, 2, [32768, 32768, 16384, 4096], 32768, seed=7)
 
 
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_attention_both_f16_kernels(kernel, monkeypatch):
+    """The vector-ALU and matrix-core partial kernels (chosen by context
+    length; LKHIP_ATTN forces one) on the same cases, short and long."""
+    monkeypatch.setenv("LKHIP_ATTN", kernel)
+    _attn_case(1, 14, 2, [1], 64, seed=11)
+    _attn_case(3, 9, 3, [300, 17, 1000], 1024, seed=12)
+    _attn_case(4, 32, 4, [4096, 1, 2500, 777], 4096, seed=13)
+    _attn_case(2, 14, 2, [16384, 9999], 16384, seed=14)
+
+
 def test_argmax_first_max_wins():
     x = np.random.default_rng(1).standard_normal((3, 151936)).astype(np.float32)
     x[1, 500] = x[1, 900] = 100.0
