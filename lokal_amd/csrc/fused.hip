@@ -448,7 +448,12 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             // in bounds; rows >= pos are replaced (pos) or masked (> pos) below.
             // One base address per lane, the rest immediate offsets.
             uint4 kraw[KC], vraw[KC];
-            const KV* Kl = K + (t * 64u + (uint32_t)lane) * 64u;
+            // K rows from pos on are this token's (in flight from S1) or
+            // unwritten: read row pos - 1 instead (the lane's score is
+            // replaced or masked below)
+            uint32_t krow = t * 64u + (uint32_t)lane;
+            krow = krow < pos ? krow : (pos ? pos - 1 : 0);
+            const KV* Kl = K + krow * 64u;
             const KV* Vl = V + (t * 64u + sub) * 64u + dq;
             auto load_k = [&](uint32_t) {
 #pragma unroll
@@ -488,10 +493,11 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             {
                 const uint32_t p = t * 64 + (uint32_t)lane;
                 const bool valid = p <= pos;
-                if (p == pos) {  // this token's k packed like a cache row: one code path below
-#pragma unroll
-                    for (int q = 0; q < KC; q++) kraw[q] = pack4(wk + q * (KV32 ? 4 : 8), KV32);
-                }
+                // this token's k (lane p == pos) comes from LDS: its cache row
+                // is being written in this stage.  Selected per value rather
+                // than written into kraw, which would make the wave wait for
+                // every load still in flight into those registers (the V tile).
+                const bool cur = p == pos;
                 float s = 0.f;
 #pragma unroll
                 for (int q = 0; q < 8; q++) {  // 8 dims at a time
@@ -503,6 +509,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     s = fmaf(k8[2], qa.z, s); s = fmaf(k8[3], qa.w, s);
                     s = fmaf(k8[4], qb.x, s); s = fmaf(k8[5], qb.y, s);
                     s = fmaf(k8[6], qb.z, s); s = fmaf(k8[7], qb.w, s);
+                }
+                if (has_cur) {  // wave-uniform: lane = dim, then the wave sum
+                    const float sc = lk_wave_sum(wk[lane] * wq[lane]);
+                    if (cur) s = sc;
                 }
                 LKF_SUB(3);
                 if constexpr (KV32) load_v(t);
@@ -518,17 +528,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) {
                     const uint32_t pj = t * 64 + jj * 8 + sub;
-                    if (pj == pos) {  // this token's v from LDS, packed like a cache chunk
-                        if constexpr (KV32) {
-                            vraw[2 * jj] = pack4(wvc + dq, true);
-                            vraw[2 * jj + 1] = pack4(wvc + dq + 4, true);
-                        } else {
-                            vraw[jj] = pack4(wvc + dq, false);
-                        }
-                    }
                     if (pj <= pos) {
                         float v8[8];
                         unpack8(vraw, jj, KV32, v8);
+                        if (pj == pos) {  // this token's v from LDS (as k above)
+                            const float4 va = *(const float4*)(wvc + dq), vb = *(const float4*)(wvc + dq + 4);
+                            v8[0] = va.x; v8[1] = va.y; v8[2] = va.z; v8[3] = va.w;
+                            v8[4] = vb.x; v8[5] = vb.y; v8[6] = vb.z; v8[7] = vb.w;
+                        }
                         const float pw = wP[sub * 8 + jj];
 #pragma unroll
                         for (int e = 0; e < 8; e++) acc[e] = fmaf(pw, v8[e], acc[e]);
@@ -594,6 +601,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     for (int k = 0; k < 16; k++)
                         if ((uint32_t)(wa[k] >> 32) != ep) wa[k] = ld_word(pp + (k0 + k) * 66 + 2 + lane);
                 }
+                if (k0 == 0) LKF_SUB(20);
                 if (k0 == 0) {
                     if (mk) {
                         mv = __uint_as_float((uint32_t)wmw);
@@ -612,6 +620,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     }
                 }
             }
+            LKF_SUB(21);
             publish(AB + hq * 64 + lane, A / Ls, ep);
         }
         LKF_MARK(2 + 6 * L + 2);
