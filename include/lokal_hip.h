@@ -39,8 +39,12 @@ enum {
 enum {
     LKHIP_F32 = 0,
     LKHIP_F16 = 1,
+    LKHIP_Q4_0 = 2,
+    LKHIP_Q5_0 = 6,
     LKHIP_Q8_0 = 8,
-    LKHIP_Q4_K = 12
+    LKHIP_Q4_K = 12,
+    LKHIP_Q5_K = 13,
+    LKHIP_Q6_K = 14
 };
 
 /* ModelConfig, src/config.rs:10-30 (the fields the decode step reads).
@@ -207,7 +211,11 @@ int lkhip_event_elapsed_ms(void* start, void* stop, float* ms);
 /* ----------------------------------------------------------- kernels */
 
 /* A weight matrix uploaded once in its GGUF type and repacked for the device
- * (values unchanged).  type F16, Q8_0 or Q4_K; host bytes are GGUF rows. */
+ * (values unchanged).  type F16, Q8_0, Q4_0, Q5_0, Q4_K, Q5_K or Q6_K; host
+ * bytes are GGUF rows (src/gguf/dequant.rs:191-535 reads the same bytes).
+ * Q4_0 / Q5_0 are stored as int8 + f16 scale, Q5_K / Q6_K as int8 + an f32
+ * (scale, min) pair per 16 values: the same values at 1.06 / 1.5 device bytes
+ * per weight. */
 int lkhip_weight_create(uint32_t ggml_type, size_t rows, size_t cols, const void* host_bytes, size_t nbytes,
                         lkhip_weight** out);
 void lkhip_weight_destroy(lkhip_weight* w);

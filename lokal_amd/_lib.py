@@ -14,6 +14,7 @@ LIB_PATH = Path(os.environ.get("LOKAL_HIP_LIB") or Path(__file__).resolve().pare
 
 LKHIP_OK = 0
 LKHIP_F32, LKHIP_F16, LKHIP_Q8_0, LKHIP_Q4_K = 0, 1, 8, 12
+LKHIP_Q4_0, LKHIP_Q5_0, LKHIP_Q5_K, LKHIP_Q6_K = 2, 6, 13, 14
 
 
 class LokalHipError(RuntimeError):

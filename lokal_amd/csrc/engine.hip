@@ -19,6 +19,7 @@
 #include "lkhip_common.h"
 #include "fused.h"
 #include "gguf.h"
+#include "repack.h"
 
 // ------------------------------------------------------------------ errors
 
@@ -58,35 +59,23 @@ struct lkhip_weight {
     void* data = nullptr;
     void* aux = nullptr;
     double bytes = 0;  // algorithmic bytes in the GGUF type
+    uint32_t ggml_type = 0;  // the GGUF type (dw.type is the device form)
     ~lkhip_weight() {
         if (data) (void)hipFree(data);
         if (aux) (void)hipFree(aux);
     }
 };
 
-static size_t blk_elems(uint32_t t) {
-    switch (t) {
-    case LKHIP_F32: case LKHIP_F16: return 1;
-    case LKHIP_Q8_0: return 32;
-    case LKHIP_Q4_K: return 256;
-    default: return 0;
-    }
-}
-static size_t blk_bytes(uint32_t t) {
-    switch (t) {
-    case LKHIP_F32: return 4;
-    case LKHIP_F16: return 2;
-    case LKHIP_Q8_0: return 34;
-    case LKHIP_Q4_K: return 144;
-    default: return 0;
-    }
-}
+using lkr::blk_bytes;
+using lkr::blk_elems;
+
 static const char* type_name(uint32_t t) {
     switch (t) {
     case LKHIP_F32: return "F32";
     case LKHIP_F16: return "F16";
     case LKHIP_Q8_0: return "Q8_0";
     case LKHIP_Q4_K: return "Q4_K";
+    case LK_Q8_SM: return "Q8_SM (device form of Q5_K / Q6_K)";
     case 2: return "Q4_0";
     case 6: return "Q5_0";
     case 13: return "Q5_K";
@@ -110,7 +99,7 @@ static int weight_create(uint32_t type, size_t rows, size_t cols, const void* ho
     if (!host || !out || rows == 0 || cols == 0) return fail(LKHIP_E_INVALID, "weight: empty tensor or null pointer");
     if (blk_elems(type) == 0)
         return fail(LKHIP_E_UNSUPPORTED,
-                    "tensor type %s is not supported by the hip backend — re-quantize as Q8_0 or Q4_K (or F16)",
+                    "tensor type %s is not supported by the hip backend — it takes F16, Q8_0, Q4_0, Q5_0, Q4_K, Q5_K and Q6_K",
                     type_name(type));
     if (cols % blk_elems(type))
         return fail(LKHIP_E_INVALID, "weight: %zu columns is not a whole number of %s blocks", cols, type_name(type));
@@ -124,38 +113,19 @@ static int weight_create(uint32_t type, size_t rows, size_t cols, const void* ho
     if (unpermute_hd && rows % unpermute_hd) return fail(LKHIP_E_INVALID, "unpermute: rows not a multiple of head_dim");
 
     auto w = std::make_unique<lkhip_weight>();
-    w->dw.type = type;
+    const uint32_t dev = lkr::device_type(type);
+    w->ggml_type = type;
+    w->dw.type = dev;
     w->dw.rows = (uint32_t)rows;
     w->dw.cols = (uint32_t)cols;
     w->bytes = (double)nbytes;
     const uint8_t* src = (const uint8_t*)host;
-    size_t data_row = 0, aux_row = 0;
-    switch (type) {
-    case LKHIP_F32: data_row = cols * 4; break;
-    case LKHIP_F16: data_row = cols * 2; break;
-    case LKHIP_Q8_0: data_row = cols; aux_row = cols / 32 * 2; break;
-    case LKHIP_Q4_K: data_row = cols / 256 * 128; aux_row = cols / 256 * 16; break;
-    }
+    const size_t data_row = lkr::data_row_bytes(dev, cols), aux_row = lkr::aux_row_bytes(dev, cols);
     std::vector<uint8_t> hd(rows * data_row), ha(rows * aux_row);
     auto repack = [&](size_t r0, size_t r1) {
-        for (size_t r = r0; r < r1; r++) {
-            const uint8_t* s = src + src_row(r, unpermute_hd) * row_bytes;
-            uint8_t* d = hd.data() + r * data_row;
-            uint8_t* a = ha.data() + r * aux_row;
-            if (type == LKHIP_F32 || type == LKHIP_F16) {
-                memcpy(d, s, row_bytes);
-            } else if (type == LKHIP_Q8_0) {
-                for (size_t b = 0; b < cols / 32; b++) {
-                    memcpy(a + 2 * b, s + 34 * b, 2);
-                    memcpy(d + 32 * b, s + 34 * b + 2, 32);
-                }
-            } else {
-                for (size_t b = 0; b < cols / 256; b++) {
-                    memcpy(a + 16 * b, s + 144 * b, 16);
-                    memcpy(d + 128 * b, s + 144 * b + 16, 128);
-                }
-            }
-        }
+        for (size_t r = r0; r < r1; r++)
+            lkr::repack_row(type, src + src_row(r, unpermute_hd) * row_bytes, cols, hd.data() + r * data_row,
+                            ha.data() + r * aux_row);
     };
     const size_t nt = rows * row_bytes > (8u << 20) ? 8 : 1;
     std::vector<std::thread> th;
@@ -220,6 +190,11 @@ struct Layer {
     bool has_bias = false;
 };
 
+// q, k and v stored in different device types: they cannot share one launch.
+static bool qkv_mixed(const Layer& ly) {
+    return ly.k->dw.type != ly.q->dw.type || ly.v->dw.type != ly.q->dw.type;
+}
+
 struct lkhip_engine {
     lkhip_config cfg{};
     uint32_t hd = 0, qd = 0, kvd = 0;
@@ -253,21 +228,8 @@ static int upload_vec(DevBuf& b, const lkhip_tensor* t, size_t n, const char* wh
         memcpy(h.data(), t->data, n * 4);
     } else if (t->ggml_type == LKHIP_F16) {
         if (t->nbytes != n * 2) return fail(LKHIP_E_INVALID, "%s: byte size mismatch", t->name);
-        const uint16_t* s = (const uint16_t*)t->data;
-        for (size_t i = 0; i < n; i++) {
-            // exact f16 -> f32
-            uint32_t hbits = s[i], sign = (hbits >> 15) << 31, e = (hbits >> 10) & 31, m = hbits & 1023, bits;
-            if (e == 0) {
-                if (m == 0) bits = sign;
-                else {
-                    int k = -1;
-                    do { m <<= 1; k++; } while (!(m & 1024));
-                    bits = sign | ((uint32_t)(112 - k) << 23) | ((m & 1023) << 13);
-                }
-            } else if (e == 31) bits = sign | 0x7f800000u | (m << 13);
-            else bits = sign | ((e + 112) << 23) | (m << 13);
-            memcpy(&h[i], &bits, 4);
-        }
+        const uint8_t* s = (const uint8_t*)t->data;
+        for (size_t i = 0; i < n; i++) h[i] = lkr::h2f(lkr::u16_at(s + 2 * i));
     } else {
         return fail(LKHIP_E_UNSUPPORTED, "%s: norm/bias tensors must be F32 or F16, got %s", t->name,
                     type_name(t->ggml_type));
@@ -317,7 +279,7 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "lm_head type differs from the layer weights";
         return LKHIP_OK;
     }
-    const uint32_t ce = wt == LKHIP_Q8_0 ? 16 : wt == LKHIP_F16 ? 8 : 32;
+    const uint32_t ce = (wt == LKHIP_Q8_0 || wt == LK_Q8_SM) ? 16 : wt == LKHIP_F16 ? 8 : 32;
     const uint32_t h = c.hidden_size, I = c.intermediate_size;
     if (e->qd != h) {
         e->fused_why = "q width differs from hidden size";
@@ -403,7 +365,6 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
     const size_t uhd = llama_permuted ? e->hd : 0;
     e->layers.resize(cfg->num_hidden_layers);
     int rc;
-    uint32_t mv_type = 0;
     for (uint32_t L = 0; L < cfg->num_hidden_layers; L++) {
         Layer& ly = e->layers[L];
         std::string p = "model.layers." + std::to_string(L) + ".";
@@ -433,17 +394,14 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
             if ((rc = upload_vec(ly.bv, bv ? bv : &zk, e->kvd, "v bias"))) return rc;
             ly.has_bias = true;
         }
-        const uint32_t t = ly.q->dw.type;
-        if (ly.k->dw.type != t || ly.v->dw.type != t)
-            return fail(LKHIP_E_UNSUPPORTED, "layer %u: q/k/v weights must share one type for the fused QKV matvec", L);
+        // q/k/v of different types (Q4_K_M files store some v in Q6_K) run
+        // as one launch per projection; gate and up share the SwiGLU launch
         if (ly.gate->dw.type != ly.up->dw.type)
             return fail(LKHIP_E_UNSUPPORTED, "layer %u: gate/up weights must share one type for the fused SwiGLU matvec",
                         L);
-        mv_type = t;
         for (auto* w : {ly.q.get(), ly.k.get(), ly.v.get(), ly.o.get(), ly.gate.get(), ly.up.get(), ly.down.get()})
             e->matvec_bytes += w->bytes;
     }
-    (void)mv_type;
     if ((rc = upload_mat(e->embed, find("model.embed_tokens.weight"), cfg->vocab_size, h, 0, "embed_tokens")))
         return rc;
     if ((rc = upload_vec(e->norm, find("model.norm.weight"), h, "model.norm.weight"))) return rc;
@@ -650,13 +608,28 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         Layer& ly = e->layers[L];
         STEP(lk_rmsnorm_launch(x, ly.in_norm.as<float>(), 1, h, c.rms_norm_eps, xn, st), C_OTHER, 0);
         {
-            LkMvArgs a = mv_args(xn, h);
-            a.nseg = 3;
-            a.seg[0] = {ly.q->dw, ly.has_bias ? ly.bq.as<float>() : nullptr, qkv};
-            a.seg[1] = {ly.k->dw, ly.has_bias ? ly.bk.as<float>() : nullptr, qkv + e->qd};
-            a.seg[2] = {ly.v->dw, ly.has_bias ? ly.bv.as<float>() : nullptr, qkv + e->qd + e->kvd};
-            a.total_rows = e->qd + 2 * e->kvd;
-            STEP(lk_matvec_launch(a, LK_MV_STORE, st), C_MATVEC, ly.q->bytes + ly.k->bytes + ly.v->bytes);
+            const LkSeg sq{ly.q->dw, ly.has_bias ? ly.bq.as<float>() : nullptr, qkv};
+            const LkSeg sk{ly.k->dw, ly.has_bias ? ly.bk.as<float>() : nullptr, qkv + e->qd};
+            const LkSeg sv{ly.v->dw, ly.has_bias ? ly.bv.as<float>() : nullptr, qkv + e->qd + e->kvd};
+            if (!qkv_mixed(ly)) {
+                LkMvArgs a = mv_args(xn, h);
+                a.nseg = 3;
+                a.seg[0] = sq;
+                a.seg[1] = sk;
+                a.seg[2] = sv;
+                a.total_rows = e->qd + 2 * e->kvd;
+                STEP(lk_matvec_launch(a, LK_MV_STORE, st), C_MATVEC, ly.q->bytes + ly.k->bytes + ly.v->bytes);
+            } else {
+                const LkSeg segs[3] = {sq, sk, sv};
+                const lkhip_weight* ws[3] = {ly.q.get(), ly.k.get(), ly.v.get()};
+                for (int i = 0; i < 3; i++) {
+                    LkMvArgs a = mv_args(xn, h);
+                    a.nseg = 1;
+                    a.seg[0] = segs[i];
+                    a.total_rows = segs[i].w.rows;
+                    STEP(lk_matvec_launch(a, LK_MV_STORE, st), C_MATVEC, ws[i]->bytes);
+                }
+            }
         }
         const size_t kv_el = s->kv_f32 ? 4 : 2;
         uint8_t* kc = s->kc.as<uint8_t>() + (size_t)L * kv_layer_elems(s) * kv_el;
@@ -1027,6 +1000,9 @@ static size_t rows_gemm_part(const lkhip_engine* e, uint32_t cap) {
             lk_gemm_plan(l0.down->dw.type, h, I, n, LK_MV_ACC),
             lk_gemm_plan(e->lm_head->dw.type, c.vocab_size, h, n < LK_ROWS_LOGITS ? n : LK_ROWS_LOGITS, LK_MV_STORE)};
         for (const auto& q : p) need = std::max(need, q.part_floats);
+        if (qkv_mixed(l0))
+            for (const lkhip_weight* w : {l0.q.get(), l0.k.get(), l0.v.get()})
+                need = std::max(need, lk_gemm_plan(w->dw.type, w->dw.rows, h, n, LK_MV_STORE).part_floats);
     }
     return need;
 }
@@ -1035,7 +1011,8 @@ static int rows_check_engine(const lkhip_engine* e) {
     const lkhip_config& c = e->cfg;
     const uint32_t h = c.hidden_size, I = c.intermediate_size;
     for (const Layer& ly : e->layers) {
-        if (!lk_gemm_shape_ok(ly.q->dw.type, e->qd + 2 * e->kvd, h) || !lk_gemm_shape_ok(ly.o->dw.type, h, e->qd) ||
+        if (!lk_gemm_shape_ok(ly.q->dw.type, e->qd + 2 * e->kvd, h) || !lk_gemm_shape_ok(ly.k->dw.type, e->kvd, h) ||
+            !lk_gemm_shape_ok(ly.v->dw.type, e->kvd, h) || !lk_gemm_shape_ok(ly.o->dw.type, h, e->qd) ||
             !lk_gemm_shape_ok(ly.gate->dw.type, I, h) || !lk_gemm_shape_ok(ly.down->dw.type, h, I))
             return fail(LKHIP_E_UNSUPPORTED,
                         "the batched path needs hidden and intermediate widths that are multiples of 32 (256 for "
@@ -1110,7 +1087,19 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.ldx = h;
             a.ldy = qkvd;
             a.part = part;
-            RSTEP(lk_gemm_launch(a, LK_MV_STORE, st, &ks));
+            if (!qkv_mixed(ly)) {
+                RSTEP(lk_gemm_launch(a, LK_MV_STORE, st, &ks));
+            } else {
+                // one GEMM per projection, each reduced (bias included) into
+                // qkv, so the RoPE pass reads finished rows (ks = 0)
+                const LkSeg segs[3] = {a.seg[0], a.seg[1], a.seg[2]};
+                for (int i = 0; i < 3; i++) {
+                    a.nseg = 1;
+                    a.seg[0] = segs[i];
+                    a.N = segs[i].w.rows;
+                    RSTEP(lk_gemm_launch(a, LK_MV_STORE, st));
+                }
+            }
         }
         uint8_t* kc = kv.kc + L * kv.layer_bytes;
         uint8_t* vc = kv.vc + L * kv.layer_bytes;
@@ -1602,12 +1591,12 @@ extern "C" int lkhip_matvec(const lkhip_weight* w, const float* x, const float* 
 }
 extern "C" int lkhip_q8_0_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
                                  void* stream) {
-    if (w && w->dw.type != LKHIP_Q8_0) return fail(LKHIP_E_INVALID, "q8_0_matvec: weight is %s", type_name(w->dw.type));
+    if (w && w->ggml_type != LKHIP_Q8_0) return fail(LKHIP_E_INVALID, "q8_0_matvec: weight is %s", type_name(w->ggml_type));
     return lkhip_matvec(w, x, bias, y, accumulate, stream);
 }
 extern "C" int lkhip_q4_k_matvec(const lkhip_weight* w, const float* x, const float* bias, float* y, int accumulate,
                                  void* stream) {
-    if (w && w->dw.type != LKHIP_Q4_K) return fail(LKHIP_E_INVALID, "q4_k_matvec: weight is %s", type_name(w->dw.type));
+    if (w && w->ggml_type != LKHIP_Q4_K) return fail(LKHIP_E_INVALID, "q4_k_matvec: weight is %s", type_name(w->ggml_type));
     return lkhip_matvec(w, x, bias, y, accumulate, stream);
 }
 

@@ -1,6 +1,6 @@
 // gemm.hip -- the multi-row dequant-fused linear layer on the matrix cores:
 // Y[b][n] = sum_k X[b][k] * W[n][k] (+ bias[n]) for b < B rows of f32
-// activations, W in its GGUF type (F16, Q8_0, Q4_K) dequantized as it is
+// activations, W in its device type (F16, Q8_0, Q4_K, Q8_SM) dequantized as it is
 // loaded.  This is Linear::forward (src/model.rs:27-35) applied to a batch of
 // tokens: the Batcher's decode step (one row per sequence, src/engine.rs:42-47)
 // and chunked prefill (rows = prompt positions of one sequence), the work
@@ -40,6 +40,7 @@ template <int WT> struct Raw;
 template <> struct Raw<LK_Q8_0> { uint4 q[2]; uint32_t d; };
 template <> struct Raw<LK_F16> { uint4 q[4]; };
 template <> struct Raw<LK_Q4_K> { uint4 q[2]; uint4 hd; };
+template <> struct Raw<LK_Q8_SM> { uint4 q[2]; uint4 sm; };  // (s, m) of the lane's two 16-weight groups
 
 // Raw bytes of the 32 weights (row r, columns kb..kb+31) of one lane.
 template <int WT>
@@ -49,6 +50,11 @@ __device__ __forceinline__ void raw_load(Raw<WT>& R, const LkDevW& w, uint32_t r
         R.q[0] = p[0];
         R.q[1] = p[1];
         R.d = ((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + kb / 32];
+    } else if constexpr (WT == LK_Q8_SM) {
+        const uint4* p = (const uint4*)(w.data + (size_t)r * w.cols + kb);
+        R.q[0] = p[0];
+        R.q[1] = p[1];
+        R.sm = *(const uint4*)(w.aux + ((size_t)r * (w.cols / 16) + kb / 16) * 8);
     } else if constexpr (WT == LK_F16) {
         const uint4* p = (const uint4*)(w.data + ((size_t)r * w.cols + kb) * 2);
 #pragma unroll
@@ -67,7 +73,8 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
 }
 
 // Weights 8*s .. 8*s+7 of the lane's 32 as exact f32 (dequant_row_ref,
-// src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K); zero when
+// src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K, :484-533
+// Q5_K / Q6_K as Q8_SM); zero when
 // the lane's columns lie past K.
 template <int WT>
 __device__ __forceinline__ void dequant8(const Raw<WT>& R, int s, uint32_t kb, bool ok, float* w) {
@@ -79,6 +86,17 @@ __device__ __forceinline__ void dequant8(const Raw<WT>& R, int s, uint32_t kb, b
         for (int t = 0; t < 4; t++) {
             w[t] = __fmul_rn((float)((int32_t)(w0 << (24 - 8 * t)) >> 24), d);
             w[4 + t] = __fmul_rn((float)((int32_t)(w1 << (24 - 8 * t)) >> 24), d);
+        }
+    } else if constexpr (WT == LK_Q8_SM) {
+        // weights 8s..8s+7 lie in group s >> 1: y = s*q - m
+        const float sv = __uint_as_float(s < 2 ? R.sm.x : R.sm.z), mv = __uint_as_float(s < 2 ? R.sm.y : R.sm.w);
+        const uint4 v = R.q[s >> 1];
+        const uint32_t w0 = word_of(v, (s & 1) * 2), w1 = word_of(v, (s & 1) * 2 + 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float q0 = (float)((int32_t)(w0 << (24 - 8 * t)) >> 24), q1 = (float)((int32_t)(w1 << (24 - 8 * t)) >> 24);
+            w[t] = ok ? __fsub_rn(__fmul_rn(sv, q0), mv) : 0.f;
+            w[4 + t] = ok ? __fsub_rn(__fmul_rn(sv, q1), mv) : 0.f;
         }
     } else if constexpr (WT == LK_F16) {
         const uint4 v = R.q[s];
@@ -331,7 +349,7 @@ LkGemmPlan lk_gemm_plan(uint32_t type, uint32_t N, uint32_t K, uint32_t n_rows, 
 bool lk_gemm_shape_ok(uint32_t type, uint32_t N, uint32_t K) {
     if (N == 0 || K == 0 || K % 32) return false;
     if (type == LK_Q4_K && K % 256) return false;
-    return type == LK_Q8_0 || type == LK_F16 || type == LK_Q4_K;
+    return type == LK_Q8_0 || type == LK_F16 || type == LK_Q4_K || type == LK_Q8_SM;
 }
 
 hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st, uint32_t* deferred_ks) {
@@ -354,6 +372,7 @@ hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st, uint32_t* defe
     switch (type) {
     case LK_Q8_0: e = lkg::launch_t<LK_Q8_0>(a, mode, p.mb, grid, st); break;
     case LK_F16: e = lkg::launch_t<LK_F16>(a, mode, p.mb, grid, st); break;
+    case LK_Q8_SM: e = lkg::launch_t<LK_Q8_SM>(a, mode, p.mb, grid, st); break;
     default: e = lkg::launch_t<LK_Q4_K>(a, mode, p.mb, grid, st); break;
     }
     if (deferred_ks) *deferred_ks = a.ks > 1 ? a.ks : 0;

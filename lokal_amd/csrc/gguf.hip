@@ -43,8 +43,9 @@ TypeSize type_size(uint32_t t) {
     default: return {0, 0, nullptr};
     }
 }
-// Types the hip backend uploads: matrices F16 / Q8_0 / Q4_K, vectors F32 / F16.
-bool runs(uint32_t t) { return t == 0 || t == 1 || t == 8 || t == 12; }
+// Types the hip backend uploads: matrices F16 / Q8_0 / Q4_0 / Q5_0 / Q4_K /
+// Q5_K / Q6_K, vectors F32 / F16.
+bool runs(uint32_t t) { return t == 0 || t == 1 || t == 2 || t == 6 || t == 8 || (t >= 12 && t <= 14); }
 
 struct Value {
     enum Kind { U, I, F, B, S, ARR } kind = U;
@@ -279,7 +280,7 @@ int lk_gguf_open(const char* path, LkGguf* g, std::string* err) {
         *err = "this checkpoint uses " + std::to_string(unsupported.size()) +
                " weight type(s) the hip backend does not run, across " + std::to_string(total) + " of " +
                std::to_string(n_tensors) + " tensors: " + detail +
-               ". Re-export the model with Q8_0, Q4_K or F16 matrices.";
+               ". Re-export the model with F16, Q8_0, Q4_0, Q5_0, Q4_K, Q5_K or Q6_K matrices.";
         return fail(LKHIP_E_UNSUPPORTED);
     }
 

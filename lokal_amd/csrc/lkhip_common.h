@@ -8,8 +8,10 @@
 
 #define LK_WAVE 64
 
-// Weight types as stored on the device (GGUF ids; values unchanged, layout repacked).
-enum LkType : uint32_t { LK_F32 = 0, LK_F16 = 1, LK_Q8_0 = 8, LK_Q4_K = 12 };
+// Weight types as stored on the device (GGUF ids; values unchanged, layout
+// repacked).  LK_Q8_SM is not a GGUF type: it is the device form of Q6_K and
+// Q5_K (see LkDevW).  Q4_0 and Q5_0 are stored as LK_Q8_0.
+enum LkType : uint32_t { LK_F32 = 0, LK_F16 = 1, LK_Q8_0 = 8, LK_Q4_K = 12, LK_Q8_SM = 64 };
 
 // f16 bits -> f32, exact (IEEE conversion; what half::f16::to_f32 computes,
 // src/gguf/dequant.rs:135-137).
@@ -77,6 +79,12 @@ __device__ __forceinline__ uint32_t lk_argmax_idx(uint64_t key) { return 0xFFFFF
 //   Q8_0 : data = int8  [rows][cols]          aux = half [rows][cols/32]  (block scales d)
 //   Q4_K : data = uint8 [rows][cols/256][128] aux = uint8 [rows][cols/256][16]
 //          (aux = the super-block head: d, dmin f16 + 12 packed 6-bit scale/min bytes)
+//   Q8_SM: data = int8  [rows][cols]          aux = float2 [rows][cols/16]  (s, m per 16)
+//          y = s*q - m, the product rounded before the subtraction.  Q6_K
+//          (y = (d*sc)*q, src/gguf/dequant.rs:510-533) stores s = d*sc, m = 0;
+//          Q5_K (y = d1*q - m1, :484-509) stores s = d1, m = m1.  Both
+//          products d*sc, dmin*m of an f16 and a 6/8-bit integer are exact in
+//          f32, so the stored pair reproduces the reference's values bit for bit.
 struct LkDevW {
     uint32_t type;
     uint32_t rows, cols;

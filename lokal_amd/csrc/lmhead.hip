@@ -163,22 +163,26 @@ uint32_t lk_lm_head_blocks(uint32_t vocab, uint32_t type, uint32_t h) {
     return need < LK_HEAD_MAX_BLOCKS ? (need ? need : 1) : LK_HEAD_MAX_BLOCKS;
 }
 
+static uint32_t head_chunk_elems(uint32_t type) {
+    return (type == LK_Q8_0 || type == LK_Q8_SM) ? 16 : (type == LK_F16 ? 8 : 32);
+}
+
 uint32_t lk_lm_head_rows(uint32_t type, uint32_t h) {
-    const uint32_t elems = type == LK_Q8_0 ? 16 : (type == LK_F16 ? 8 : 32);
+    const uint32_t elems = head_chunk_elems(type);
     const uint32_t nch = (h / elems + 63) / 64;
     return nch > 1 ? 2 : 4;
 }
 
 bool lk_lm_head_fits(uint32_t type, uint32_t h) {
-    if (type != LK_Q8_0 && type != LK_F16 && type != LK_Q4_K) return false;
-    const uint32_t elems = type == LK_Q8_0 ? 16 : (type == LK_F16 ? 8 : 32);
+    if (type != LK_Q8_0 && type != LK_F16 && type != LK_Q4_K && type != LK_Q8_SM) return false;
+    const uint32_t elems = head_chunk_elems(type);
     return h > 0 && h % elems == 0 && (h / elems + 63) / 64 <= 4;
 }
 
 hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t st) {
     if (!lk_lm_head_fits(a.w.type, a.h) || blocks == 0 || blocks > LK_HEAD_MAX_BLOCKS) return hipErrorInvalidValue;
     const uint32_t t = a.w.type;
-    const uint32_t elems = t == LK_Q8_0 ? 16 : (t == LK_F16 ? 8 : 32);
+    const uint32_t elems = head_chunk_elems(t);
     const uint32_t nch = (a.h / elems + 63) / 64;
 #define LKH_NCH(T)                                                    \
     switch (nch) {                                                    \
@@ -191,6 +195,7 @@ hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t s
     if (t == LK_Q8_0) { LKH_NCH(LK_Q8_0) }
     if (t == LK_F16) { LKH_NCH(LK_F16) }
     if (t == LK_Q4_K) { LKH_NCH(LK_Q4_K) }
+    if (t == LK_Q8_SM) { LKH_NCH(LK_Q8_SM) }
 #undef LKH_NCH
     return hipErrorInvalidValue;
 }

@@ -5,7 +5,7 @@
 
 static uint32_t chunk_elems(uint32_t type) {
     switch (type) {
-    case LK_Q8_0: return 16;
+    case LK_Q8_0: case LK_Q8_SM: return 16;
     case LK_F16: return 8;
     case LK_Q4_K: return 32;
     default: return 0;
@@ -50,6 +50,7 @@ hipError_t lk_matvec_launch(const LkMvArgs& a, int mode, hipStream_t st, LkMvPla
     case LK_Q8_0: return lk_matvec_launch_q8_0(a, mode, p.rows_per_wave, p.nch, p.blocks, st);
     case LK_F16: return lk_matvec_launch_f16(a, mode, p.rows_per_wave, p.nch, p.blocks, st);
     case LK_Q4_K: return lk_matvec_launch_q4_k(a, mode, p.rows_per_wave, p.nch, p.blocks, st);
+    case LK_Q8_SM: return lk_matvec_launch_q8_sm(a, mode, p.rows_per_wave, p.nch, p.blocks, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -1,9 +1,9 @@
 // matvec_impl.h -- the dequant-fused matvec kernel, one template for every
-// weight type.  Included by matvec_{q8_0,f16,q4_k}.hip, each of which
-// instantiates it for one type so the three compile in parallel.
+// weight type.  Included by matvec_{q8_0,f16,q4_k,q8_sm}.hip, each of which
+// instantiates it for one type so they compile in parallel.
 //
 // Work split: one wave (64 lanes) owns R output rows.  A row's payload is cut
-// into 16-byte "chunks" (Q8_0: 16 weights, F16: 8, Q4_K: 32 nibbles); lane l
+// into 16-byte "chunks" (Q8_0, Q8_SM: 16 weights, F16: 8, Q4_K: 32 nibbles); lane l
 // owns chunks l, l+64, l+128, ...  Every 16-byte chunk is one global_load_dwordx4,
 // so a wave load is one contiguous 1 KiB run of the row.  A pass issues all
 // R x NCH chunk loads of a lane before any arithmetic, so each lane keeps
@@ -21,8 +21,16 @@ template <int WT> struct ChunkTraits;
 template <> struct ChunkTraits<LK_Q8_0> { static constexpr uint32_t elems = 16; };
 template <> struct ChunkTraits<LK_F16> { static constexpr uint32_t elems = 8; };
 template <> struct ChunkTraits<LK_Q4_K> { static constexpr uint32_t elems = 32; };
+template <> struct ChunkTraits<LK_Q8_SM> { static constexpr uint32_t elems = 16; };
 
 typedef unsigned int lk_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int lk_u32x2 __attribute__((ext_vector_type(2)));
+
+// The (s, m) pair of Q8_SM chunk ch.
+__device__ __forceinline__ uint2 ld_sm(const uint8_t* ap, uint32_t ch) {
+    const lk_u32x2 v = lk_g((const lk_u32x2*)ap)[ch];
+    return make_uint2(v.x, v.y);
+}
 
 // 16-byte streaming load of weight bytes (read once per token: nontemporal).
 __device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
@@ -48,6 +56,18 @@ __device__ __forceinline__ float dot_q8(uint4 q, const float* __restrict__ x) {
     s0 = fmaf(sbyte(q.w, 0), x3.x, s0); s1 = fmaf(sbyte(q.w, 1), x3.y, s1);
     s0 = fmaf(sbyte(q.w, 2), x3.z, s0); s1 = fmaf(sbyte(q.w, 3), x3.w, s1);
     return s0 + s1;
+}
+
+// Q8_SM: 16 int8 weights sharing one (s, m): s*sum(q x) - m*sum(x), the two
+// products rounded before the subtraction, so a one-hot x yields s*q - m, the
+// stored element (dequant_row_ref of Q6_K / Q5_K, src/gguf/dequant.rs:484-533).
+__device__ __forceinline__ float dot_q8sm(uint4 q, uint2 sm, const float* __restrict__ x) {
+    const float sq = dot_q8(q, x);
+    const float4 x0 = *(const float4*)(x + 0), x1 = *(const float4*)(x + 4);
+    const float4 x2 = *(const float4*)(x + 8), x3 = *(const float4*)(x + 12);
+    const float sx = (((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w))) +
+                     (((x2.x + x2.y) + (x2.z + x2.w)) + ((x3.x + x3.y) + (x3.z + x3.w)));
+    return __fsub_rn(__fmul_rn(__uint_as_float(sm.x), sq), __fmul_rn(__uint_as_float(sm.y), sx));
 }
 
 __device__ __forceinline__ float2 h2x2(uint32_t v) {
@@ -123,7 +143,8 @@ __device__ __forceinline__ float dot_q4k(uint4 q, uint4 hdr, uint32_t k, const f
 }
 
 // One element of a weight row, exactly as dequant_row_ref computes it
-// (src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K).
+// (src/gguf/dequant.rs:199-203 F16, :231-239 Q8_0, :462-483 Q4_K,
+// :484-533 Q5_K / Q6_K as Q8_SM; Q4_0 / Q5_0 are stored as Q8_0).
 }  // namespace lk
 __device__ __forceinline__ float lk_embed_elem(const LkDevW& w, uint32_t r, uint32_t j) {
     if (w.type == LK_F16) {
@@ -147,6 +168,10 @@ __device__ __forceinline__ float lk_embed_elem(const LkDevW& w, uint32_t r, uint
         const uint32_t q = hi ? (byte >> 4) : (byte & 0x0F);
         const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
         return __fsub_rn(__fmul_rn(d1, (float)q), m1);
+    } else if (w.type == LK_Q8_SM) {
+        const int8_t q = ((const int8_t*)w.data)[(size_t)r * w.cols + j];
+        const float2 sm = ((const float2*)w.aux)[(size_t)r * (w.cols / 16) + j / 16];
+        return __fsub_rn(__fmul_rn(sm.x, (float)q), sm.y);
     } else {  // F32
         return ((const float*)w.data)[(size_t)r * w.cols + j];
     }
@@ -156,13 +181,14 @@ namespace lk {
 
 template <int WT>
 __device__ __forceinline__ size_t row_data_bytes(uint32_t cols) {
-    if constexpr (WT == LK_Q8_0) return cols;
+    if constexpr (WT == LK_Q8_0 || WT == LK_Q8_SM) return cols;
     else if constexpr (WT == LK_F16) return (size_t)cols * 2;
     else return (size_t)(cols / 256) * 128;
 }
 template <int WT>
 __device__ __forceinline__ size_t row_aux_bytes(uint32_t cols) {
     if constexpr (WT == LK_Q8_0) return (size_t)(cols / 32) * 2;
+    else if constexpr (WT == LK_Q8_SM) return (size_t)(cols / 16) * 8;
     else if constexpr (WT == LK_F16) return 0;
     else return (size_t)(cols / 256) * 16;
 }
@@ -173,6 +199,7 @@ struct Row {
     uint4 q[NCH];
     uint4 hd[NCH];  // Q4_K super-block heads
     uint32_t d[NCH];  // Q8_0 block scales, raw f16 bits: converted at use, so issuing never waits
+    uint2 sm[NCH];    // Q8_SM (s, m) bits
 };
 
 template <int WT>
@@ -199,6 +226,7 @@ __device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint
         const uint32_t ch = ch0 < nchunk ? ch0 : 0u;
         R.q[i] = ld_stream16(rp + 16u * ch);
         if constexpr (WT == LK_Q8_0) R.d[i] = (uint32_t)lk_g((const uint16_t*)ap)[ch >> 1];
+        if constexpr (WT == LK_Q8_SM) R.sm[i] = ld_sm(ap, ch);
         if constexpr (WT == LK_Q4_K) {
             const lk_u32x4 hv = *lk_g((const lk_u32x4*)(ap + 16u * (ch >> 3)));
             R.hd[i] = make_uint4(hv.x, hv.y, hv.z, hv.w);
@@ -224,6 +252,8 @@ __device__ __forceinline__ float row_dot(const Row<WT, NCH>& R, const float* x, 
             continue;
         } else if constexpr (WT == LK_F16) {
             t = dot_f16(R.q[i], x + ch * 8);
+        } else if constexpr (WT == LK_Q8_SM) {
+            t = dot_q8sm(R.q[i], R.sm[i], x + ch * 16);
         } else {
             const uint32_t sb = ch >> 3, k = ch & 7;
             t = dot_q4k(R.q[i], R.hd[i], k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
@@ -250,6 +280,8 @@ __device__ __forceinline__ float row_dot_reg(const Row<WT, NCH>& R, const float 
             continue;
         } else if constexpr (WT == LK_F16) {
             t = dot_f16(R.q[i], xr[i]);
+        } else if constexpr (WT == LK_Q8_SM) {
+            t = dot_q8sm(R.q[i], R.sm[i], xr[i]);
         } else {
             float xx[64];  // dot_q4k reads x[0..15] and x[32..47]
 #pragma unroll
@@ -337,6 +369,24 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
                     const float* xc = x + (size_t)c * 16;
 #pragma unroll
                     for (int j = 0; j < NR; j++) acc[j] = fmaf(dsc[j][i], dot_q8(wq[j][i], xc), acc[j]);
+                }
+            }
+        } else if constexpr (WT == LK_Q8_SM) {
+            uint2 sm[NR][NCH];
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+#pragma unroll
+                for (int j = 0; j < NR; j++)
+                    sm[j][i] = (c < nchunk && rv[j]) ? ld_sm(ap[j], c) : make_uint2(0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const uint32_t c = base + (uint32_t)lane + 64u * i;
+                if (c < nchunk) {
+                    const float* xc = x + (size_t)c * 16;
+#pragma unroll
+                    for (int j = 0; j < NR; j++) acc[j] += dot_q8sm(wq[j][i], sm[j][i], xc);
                 }
             }
         } else if constexpr (WT == LK_F16) {
@@ -465,3 +515,4 @@ hipError_t launch_type(const LkMvArgs& a, int mode, int R, int nch, unsigned blo
 hipError_t lk_matvec_launch_q8_0(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);
 hipError_t lk_matvec_launch_f16(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);
 hipError_t lk_matvec_launch_q4_k(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);
+hipError_t lk_matvec_launch_q8_sm(const LkMvArgs& a, int mode, int R, int nch, unsigned blocks, hipStream_t st);

@@ -62,7 +62,7 @@ class DeviceArray:
 
 
 class Weight:
-    """A weight matrix in its GGUF type (F16, Q8_0, Q4_K), resident on device."""
+    """A weight matrix in its GGUF type (F16, Q8_0, Q4_0, Q5_0, Q4_K, Q5_K, Q6_K), resident on device."""
 
     def __init__(self, ggml_type: int, rows: int, cols: int, data: np.ndarray):
         data = np.ascontiguousarray(data).view(np.uint8).reshape(-1)

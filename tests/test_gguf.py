@@ -93,20 +93,21 @@ def test_refusals(tmp_path):
 
 def test_unsupported_types_are_listed_together(tmp_path):
     tensors = synth.synth_model(TINY, synth.Q8_0, 3, tied=True)
-    # relabel two matrices as Q6_K / Q5_K with sizes that fit those types
+    # relabel two matrices as Q2_K / Q4_1 (types the backend does not take)
+    # with sizes that fit those types
     out = []
     for t in tensors:
         if t.name.endswith(("layers.0.mlp.down_proj.weight", "layers.1.mlp.down_proj.weight")):
             rows, cols = t.dims
-            out.append(synth.Tensor(t.name, 14, t.dims, np.zeros(rows * cols // 256 * 210, np.uint8)))
+            out.append(synth.Tensor(t.name, 10, t.dims, np.zeros(rows * cols // 256 * 84, np.uint8)))
         elif t.name.endswith("layers.0.mlp.up_proj.weight"):
             rows, cols = t.dims
-            out.append(synth.Tensor(t.name, 13, t.dims, np.zeros(rows * cols // 256 * 176, np.uint8)))
+            out.append(synth.Tensor(t.name, 3, t.dims, np.zeros(rows * cols // 32 * 20, np.uint8)))
         else:
             out.append(t)
     p = tmp_path / "u.gguf"
     write_gguf(p, TINY, out)
-    with pytest.raises(LokalHipError, match=r"2 weight type\(s\).*across 3 of .*Q5_K \(1 tensor.*Q6_K \(2 tensors"):
+    with pytest.raises(LokalHipError, match=r"2 weight type\(s\).*across 3 of .*Q2_K \(2 tensors.*Q4_1 \(1 tensor"):
         gguf_config(p)
 
 
