@@ -215,6 +215,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
 // FMA rate per HBM byte is close to the ALU's.
 typedef _Float16 lk_h4 __attribute__((ext_vector_type(4)));
 typedef float lk_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int lk_u4 __attribute__((ext_vector_type(4)));
 #define LK_VS 72  // LDS row stride of a staged V tile (halves)
 
 __device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
@@ -249,7 +250,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
 
     // K: sub-tile t rows p0 + 16t + c16, this lane's 32 bytes (dims 16j..16j+15);
     // V: rows p0 + 8it + (lane >> 3), bytes 16*(lane & 7) -- 1 KiB per instruction
-    uint4 kr[4][2], vr[8];
+    uint4 kr[4][2];
+    lk_u4 vr[8];  // a vector type (not the uint4 struct): held in registers, not in scratch
     if (tile_live) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -261,7 +263,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
 #pragma unroll
         for (int it = 0; it < 8; it++) {
             const uint32_t p = p0 + 8u * it + ((uint32_t)lane >> 3);
-            vr[it] = *(const uint4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
+            vr[it] = *(const lk_u4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
         }
     }
     // q of head c16 (zero past G), dims 16j + 4s .. +3 for step s, as f16 hi + lo
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
         uint16_t* vw = vs[w];
 #pragma unroll
         for (int it = 0; it < 8; it++)
-            *(uint4*)&vw[(8 * it + (lane >> 3)) * LK_VS + 8 * (lane & 7)] = vr[it];
+            *(lk_u4*)&vw[(8 * it + (lane >> 3)) * LK_VS + 8 * (lane & 7)] = vr[it];
         // ---- scores
         lk_f4 sc[4];
 #pragma unroll

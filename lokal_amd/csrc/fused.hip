@@ -415,17 +415,23 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
         }
         LKF_SUB(18);
-        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
-        if (half1) {
+        // o_proj rows (and half 1's gate/up rows) for S4 / S5: issued after
+        // this wave's attention K/V loads, so the tile is not queued behind
+        // this layer's weight stream
+        auto issue_ahead = [&]() {
+            if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
+            if (half1) {
 #pragma unroll
-            for (int k = 0; k < LKF_KB; k++) {
-                const int uu = unit_of(k);
-                if (uu < (int)U5) {
-                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
-                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                for (int k = 0; k < LKF_KB; k++) {
+                    const int uu = unit_of(k);
+                    if (uu < (int)U5) {
+                        row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
+                        row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                    }
                 }
             }
-        }
+        };
+        if (c.gw >= (int)(nh * nch)) issue_ahead();
         LKF_MARK(2 + 6 * L + 0);
         // ---------------- S2: attention partials.  Item = (query head, tile of
         // 64 positions), one wave each, spread over the grid (items past the
@@ -470,6 +476,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 if constexpr (!KV32) load_v(t);
             };
             load_tile(t);
+            issue_ahead();
             LKF_SUB(1);
             {  // this head's q; this token's k and v for the chunk that holds pos
                 const uint64_t* sq = QB + hq * 64 + lane;
@@ -498,18 +505,21 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 // than written into kraw, which would make the wave wait for
                 // every load still in flight into those registers (the V tile).
                 const bool cur = p == pos;
-                float s = 0.f;
+                // four independent chains: one wave per SIMD has nothing to
+                // hide a 64-long dependent FMA chain behind
+                float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int q = 0; q < 8; q++) {  // 8 dims at a time
                     float k8[8];
                     unpack8(kraw, q, KV32, k8);
                     const float4 qa = *(const float4*)(wq + 8 * q);
                     const float4 qb = *(const float4*)(wq + 8 * q + 4);
-                    s = fmaf(k8[0], qa.x, s); s = fmaf(k8[1], qa.y, s);
-                    s = fmaf(k8[2], qa.z, s); s = fmaf(k8[3], qa.w, s);
-                    s = fmaf(k8[4], qb.x, s); s = fmaf(k8[5], qb.y, s);
-                    s = fmaf(k8[6], qb.z, s); s = fmaf(k8[7], qb.w, s);
+                    s4[0] = fmaf(k8[0], qa.x, s4[0]); s4[1] = fmaf(k8[1], qa.y, s4[1]);
+                    s4[2] = fmaf(k8[2], qa.z, s4[2]); s4[3] = fmaf(k8[3], qa.w, s4[3]);
+                    s4[0] = fmaf(k8[4], qb.x, s4[0]); s4[1] = fmaf(k8[5], qb.y, s4[1]);
+                    s4[2] = fmaf(k8[6], qb.z, s4[2]); s4[3] = fmaf(k8[7], qb.w, s4[3]);
                 }
+                float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
                 if (has_cur) {  // wave-uniform: lane = dim, then the wave sum
                     const float sc = lk_wave_sum(wk[lane] * wq[lane]);
                     if (cur) s = sc;
@@ -525,20 +535,34 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 wP[(lane & 7) * 8 + (lane >> 3)] = pe;  // [group][jj]: a lane's 8 weights are adjacent
                 wave_sync_lds();
                 LKF_SUB(4);
+                // this lane's 8 weights in two LDS reads; no per-position
+                // branches (each would serialise an LDS round trip)
+                const float4 pwa = *(const float4*)(wP + sub * 8), pwb = *(const float4*)(wP + sub * 8 + 4);
+                const float pw8[8] = {pwa.x, pwa.y, pwa.z, pwa.w, pwb.x, pwb.y, pwb.z, pwb.w};
+                if (!has_cur) {  // wave-uniform: every position of the tile is < pos
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const uint32_t pj = t * 64 + jj * 8 + sub;
-                    if (pj <= pos) {
+                    for (int jj = 0; jj < 8; jj++) {
                         float v8[8];
                         unpack8(vraw, jj, KV32, v8);
-                        if (pj == pos) {  // this token's v from LDS (as k above)
-                            const float4 va = *(const float4*)(wvc + dq), vb = *(const float4*)(wvc + dq + 4);
-                            v8[0] = va.x; v8[1] = va.y; v8[2] = va.z; v8[3] = va.w;
-                            v8[4] = vb.x; v8[5] = vb.y; v8[6] = vb.z; v8[7] = vb.w;
-                        }
-                        const float pw = wP[sub * 8 + jj];
 #pragma unroll
-                        for (int e = 0; e < 8; e++) acc[e] = fmaf(pw, v8[e], acc[e]);
+                        for (int e = 0; e < 8; e++) acc[e] = fmaf(pw8[jj], v8[e], acc[e]);
+                    }
+                } else {
+                    // position pos takes this token's v from LDS (as k above);
+                    // positions past pos (unwritten rows) contribute nothing
+                    const float4 va = *(const float4*)(wvc + dq), vb = *(const float4*)(wvc + dq + 4);
+                    const float vc8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj++) {
+                        const uint32_t pj = t * 64 + jj * 8 + sub;
+                        float v8[8];
+                        unpack8(vraw, jj, KV32, v8);
+                        const float pw = pj <= pos ? pw8[jj] : 0.f;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const float v = pj == pos ? vc8[e] : (pj < pos ? v8[e] : 0.f);
+                            acc[e] = fmaf(pw, v, acc[e]);
+                        }
                     }
                 }
             }
