@@ -456,12 +456,11 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
     const uint32_t G = a.n_heads / a.n_kv;
     const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     dim3 grid(max_chunks, a.n_kv, a.n_seq);
-    // The matrix-core kernel is faster up to ~8k positions (4 sequences x 24
-    // layers at ctx 4096: 8.7 vs 10.6 us per launch) and slower beyond (ctx
-    // 32768: 28.4 vs 21.7 us); LKHIP_ATTN=valu / =mfma force one of them.
+    // The matrix-core kernel is the faster one at every context measured (4
+    // sequences x 24 layers: 268 vs 327 us per step at ctx 4096, 562 vs 690
+    // at 32768); LKHIP_ATTN=valu selects the vector-ALU kernel.
     const char* fe = getenv("LKHIP_ATTN");
-    const int force = fe ? (strcmp(fe, "valu") == 0 ? 1 : (strcmp(fe, "mfma") == 0 ? 2 : 0)) : 0;
-    const bool mfma = force == 2 || (force == 0 && a.max_seq <= 8192);
+    const bool mfma = !(fe && strcmp(fe, "valu") == 0);
 #define LK_ATTN_CASE(g)                                                                         \
     case g:                                                                                     \
         if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(256), 0, st, a); \

@@ -134,7 +134,6 @@ __device__ __forceinline__ void awaitN(const Ctx& c, const uint64_t* src, uint32
     }
 }
 
-// Block-cooperative: wait for n published words into LDS.
 // Block-cooperative: wait for n published words into LDS.  half < 0: every
 // wave polls; otherwise only the waves of one half (half 0: waves 0..FW/2-1,
 // half 1: the rest) do: a wave's loads retire in issue order, so the polling

@@ -233,8 +233,8 @@ def test_attention_config5_four_sequences_32k():
 
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])
 def test_attention_both_f16_kernels(kernel, monkeypatch):
-    """The vector-ALU and matrix-core partial kernels (chosen by context
-    length; LKHIP_ATTN forces one) on the same cases, short and long."""
+    """The vector-ALU and matrix-core partial kernels (the matrix-core one by
+    default, LKHIP_ATTN=valu selects the other) on the same cases, short and long."""
     monkeypatch.setenv("LKHIP_ATTN", kernel)
     _attn_case(1, 14, 2, [1], 64, seed=11)
     _attn_case(3, 9, 3, [300, 17, 1000], 1024, seed=12)
