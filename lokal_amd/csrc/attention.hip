@@ -22,7 +22,11 @@
 #include <cstring>
 
 #define LK_HD 64
+#ifndef LK_ACHUNK
 #define LK_ACHUNK 256
+#endif
+#define LK_AW (LK_ACHUNK / 64)  // waves per partial block: one 64-position tile each
+#define LK_MB 32  // chunks per merge wave and round
 
 uint32_t lk_attn_chunk(uint32_t) { return LK_ACHUNK; }
 
@@ -54,7 +58,7 @@ __device__ __forceinline__ void load8(const float* p, float* o) {
 }
 
 template <int G, typename KV>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
+__global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnArgs a) {
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t ctx = attn_ctx(a, seq);
     const uint32_t c0 = chunk * LK_ACHUNK;
@@ -66,9 +70,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
     const KV* __restrict__ V = (const KV*)a.v + kv_base;
 
     __shared__ float qs[G][LK_HD];
-    __shared__ float ps[4][G][64];      // [wave][head][group * 8 + jj]
-    __shared__ float red_m[4][G], red_l[4][G];
-    __shared__ float red_acc[4][G][LK_HD];
+    __shared__ float ps[LK_AW][G][64];      // [wave][head][group * 8 + jj]
+    __shared__ float red_m[LK_AW][G], red_l[LK_AW][G];
+    __shared__ float red_acc[LK_AW][G][LK_HD];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
         for (int i = 0; i < 8; i++) load8(krow + 8 * i, kf + 8 * i);
     }
     const float* qsrc = a.q + (size_t)seq * a.q_stride + (size_t)kvh * G * LK_HD;
-    for (int i = tid; i < G * LK_HD; i += 256) qs[i / LK_HD][i % LK_HD] = qsrc[i];
+    for (int i = tid; i < G * LK_HD; i += LK_AW * 64) qs[i / LK_HD][i % LK_HD] = qsrc[i];
     __syncthreads();
 
     // P.V lane map: position group sub = lane & 7, dims dq..dq+7 (dq = 8 * (lane >> 3))
@@ -174,14 +178,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const LkAttnArgs a) {
 
     // ---- merge the 4 tiles into one partial per query head
     float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * max_chunks + chunk) * (2 + LK_HD);
-    for (int t = tid; t < G * LK_HD; t += 256) {
+    for (int t = tid; t < G * LK_HD; t += LK_AW * 64) {
         const int g = t / LK_HD, d = t % LK_HD;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, red_m[ww][g]);
+        for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
         float L = 0.f, A = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
+        for (int ww = 0; ww < LK_AW; ww++) {
             if (red_m[ww][g] != -INFINITY) {
                 const float sc = expf(red_m[ww][g] - M);
                 L = fmaf(sc, red_l[ww][g], L);
@@ -224,7 +228,7 @@ __device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
 }
 
 template <int G>
-__global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
+__global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs a) {
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t ctx = attn_ctx(a, seq);
     const uint32_t c0 = chunk * LK_ACHUNK;
@@ -236,10 +240,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
     const uint16_t* __restrict__ V = (const uint16_t*)a.v + kv_base;
 
     // the staged V tiles, reused for the waves' O tiles once all P.V are done
-    __shared__ __align__(16) uint16_t vs[4][64 * LK_VS];
-    __shared__ float red_m[4][16], red_l[4][16];
+    __shared__ __align__(16) uint16_t vs[LK_AW][64 * LK_VS];
+    __shared__ float red_m[LK_AW][16], red_l[LK_AW][16];
     float(*red_acc)[16][LK_HD] = (float(*)[16][LK_HD])&vs[0][0];
-    static_assert(sizeof(vs) >= 4 * 16 * LK_HD * sizeof(float), "O tiles fit the V staging area");
+    static_assert(sizeof(vs) >= LK_AW * 16 * LK_HD * sizeof(float), "O tiles fit the V staging area");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -366,14 +370,14 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
 
     // ---- merge the 4 tiles into one partial per query head
     float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * max_chunks + chunk) * (2 + LK_HD);
-    for (int t = tid; t < G * LK_HD; t += 256) {
+    for (int t = tid; t < G * LK_HD; t += LK_AW * 64) {
         const int g = t / LK_HD, dd = t % LK_HD;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, red_m[ww][g]);
+        for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
         float L = 0.f, A = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
+        for (int ww = 0; ww < LK_AW; ww++) {
             if (red_m[ww][g] != -INFINITY) {
                 const float scl = expf(red_m[ww][g] - M);
                 L = fmaf(scl, red_l[ww][g], L);
@@ -391,8 +395,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(const LkAttnArgs a) {
 
 // Fold the chunk partials of one query head: out = sum_c e^{m_c-M} acc_c /
 // sum_c e^{m_c-M} l_c.  Four waves take interleaved quarters of the chunks
-// (lane = dim; 16 chunks' words in flight per lane), each folding online
-// against its own running max, and combine their (m, l, acc) in LDS.
+// (lane = dim; 32 chunks' words in flight per lane, so contexts up to 32768
+// positions take one memory round trip), each folding online against its own
+// running max, and combine their (m, l, acc) in LDS.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const LkAttnArgs a) {
     const uint32_t h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -402,30 +407,36 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const LkAttnArgs a) {
     const float* part = a.part + ((size_t)seq * a.n_heads + h) * max_chunks * (2 + LK_HD);
     __shared__ float wm[4], wl[4], wa[4][LK_HD];
     float M = -INFINITY, L = 0.f, A = 0.f;
-    for (uint32_t c0 = w * 16; c0 < nch; c0 += 64) {  // this wave's next 16 chunks
-        float mv[16], lv[16], av[16];
+    for (uint32_t c0 = w * LK_MB; c0 < nch; c0 += 4 * LK_MB) {  // this wave's next LK_MB chunks
+        // (m, l) by vector loads: lane k < 32 holds chunk c0+k's m, lane
+        // 32+k its l (uniform-address scalar loads would queue behind the
+        // scalar unit's few outstanding requests)
+        const uint32_t kk = lane & 31;
+        const bool live = c0 + kk < nch;
+        const float ml = live ? part[(size_t)(c0 + kk) * (2 + LK_HD) + (lane >> 5)] : (lane < 32 ? -INFINITY : 0.f);
+        float av[LK_MB];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < LK_MB; k++) {
             const uint32_t c = c0 + k < nch ? c0 + k : c0;  // in-range reload, dropped below
-            const float* pc = part + (size_t)c * (2 + LK_HD);
-            mv[k] = pc[0];
-            lv[k] = pc[1];
-            av[k] = pc[2 + lane];
+            av[k] = part[(size_t)c * (2 + LK_HD) + 2 + lane];
         }
-        float Mn = M;
+        float mx = lane < 32 ? ml : -INFINITY;
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (c0 + k < nch) Mn = fmaxf(Mn, mv[k]);
+        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float Mn = fmaxf(M, __shfl(mx, 0, 64));
         const float rs = expf(M - Mn);  // 0 while M is still -inf
-        L *= rs;
+        // lane k < 32: chunk k's weight e^{m_k - Mn} (0 for dead chunks)
+        const float sck = lane < 32 && live ? expf(ml - Mn) : 0.f;
+        const float lk = __shfl(ml, (int)kk + 32, 64);  // chunk kk's l
+        float ls = lane < 32 ? sck * lk : 0.f;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
+        L = fmaf(L, rs, __shfl(ls, 0, 64));
         A *= rs;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            if (c0 + k < nch) {
-                const float sc = expf(mv[k] - Mn);
-                L = fmaf(sc, lv[k], L);
-                A = fmaf(sc, av[k], A);
-            }
+        for (int k = 0; k < LK_MB; k++) {
+            const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sck), k));
+            A = fmaf(sk, av[k], A);
         }
         M = Mn;
     }
@@ -463,9 +474,9 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
     const bool mfma = !(fe && strcmp(fe, "valu") == 0);
 #define LK_ATTN_CASE(g)                                                                         \
     case g:                                                                                     \
-        if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(256), 0, st, a); \
-        else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g>), grid, dim3(256), 0, st, a);     \
-        else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(256), 0, st, a);  \
+        if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(LK_AW * 64), 0, st, a); \
+        else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g>), grid, dim3(LK_AW * 64), 0, st, a);     \
+        else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(LK_AW * 64), 0, st, a);  \
         break;
     switch (G) {
         LK_ATTN_CASE(1)
