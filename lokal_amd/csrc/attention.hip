@@ -206,21 +206,27 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 // wave), with both products on v_mfma_f32_16x16x16f16:
 //   scores : S[pos][head] = K . q, 16 positions x 16 heads (G used) per MFMA,
 //            K rows exact in f16, q split into f16 hi + lo (22 significant
-//            bits), f32 accumulation.  Lane l holds row pos0 + (l & 15) of K
-//            and dims 16*(l >> 4) .. +15 -- the same dims for q -- so a wave's
-//            K load is 16 whole 128-byte rows;
+//            bits), f32 accumulation.  MFMA row m of sub-tile t is position
+//            16t + 4(m & 3) + (m >> 2) (a fixed permutation, shared by P.V);
+//            lane l holds that row of K for m = l & 15, dims 16*(l >> 4) ..
+//            +15 -- the same dims for q -- so a wave's K load is 16 whole
+//            128-byte rows;
 //   softmax: per head (lane & 15) over the wave's 64 positions;
 //   P.V    : O[head][dim] = P . V with P straight from the score registers
 //            (lane l holds P[head l & 15][positions 4*(l >> 4) .. +3], exactly
 //            the A-operand layout), split hi + lo like q, and V read back from
-//            LDS in the B-operand layout (the tile is staged there by
-//            coalesced 16-byte loads).
+//            LDS in the B-operand layout: the tile is staged there by
+//            coalesced 16-byte loads, and a lane reads 4 dims of each of its
+//            4 positions with one 8-byte LDS read (MFMA d of a sub-tile takes
+//            dim 4n + d for column n).  With the row permutation the two
+//            16-lane groups of a half-wave read rows of opposite parity, i.e.
+//            disjoint LDS banks.
 // At GQA 7 this is ~1/5 of the vector-ALU work of the scalar kernel, whose
 // FMA rate per HBM byte is close to the ALU's.
 typedef _Float16 lk_h4 __attribute__((ext_vector_type(4)));
 typedef float lk_f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int lk_u4 __attribute__((ext_vector_type(4)));
-#define LK_VS 72  // LDS row stride of a staged V tile (halves)
+#define LK_VS 64  // LDS row stride of a staged V tile (halves)
 
 __device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
     const uint2 u = make_uint2(lo, hi);
@@ -259,7 +265,7 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
     if (tile_live) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const uint32_t p = p0 + 16u * t + c16;
+            const uint32_t p = p0 + 16u * t + 4u * (c16 & 3) + (c16 >> 2);  // MFMA row c16
             const uint4* src = (const uint4*)(K + (size_t)(p < ctx ? p : plast) * LK_HD + 16 * j);
             kr[t][0] = src[0];
             kr[t][1] = src[1];
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t p = p0 + 16u * t + 4u * j + (uint32_t)i;
+                const uint32_t p = p0 + 16u * t + 4u * (uint32_t)i + j;  // MFMA row 4j + i
                 const float v = p < ctx ? sc[t][i] * 0.125f : -INFINITY;
                 sc[t][i] = v;
                 mx = fmaxf(mx, v);
@@ -342,21 +348,25 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
         lt = sum;
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the V tile is in LDS
         __builtin_amdgcn_wave_barrier();
-        // ---- P.V: k = positions 16t + 4j + i, n = dims 16d + c16
+        // ---- P.V: k = 4j + i <-> position 16t + 4i + j, n = c16 <-> dim 4 c16 + d
 #pragma unroll
         for (int t = 0; t < 4; t++) {
+            uint2 r[4];  // dims 4 c16 .. +3 of positions 16t + 4i + j
+#pragma unroll
+            for (int i = 0; i < 4; i++) r[i] = *(const uint2*)&vw[(16 * t + 4 * i + j) * LK_VS + 4 * c16];
 #pragma unroll
             for (int d = 0; d < 4; d++) {
-                const uint16_t* vp = &vw[(16 * t + 4 * j) * LK_VS + 16 * d + c16];
-                const uint32_t v01 = (uint32_t)vp[0] | ((uint32_t)vp[LK_VS] << 16);
-                const uint32_t v23 = (uint32_t)vp[2 * LK_VS] | ((uint32_t)vp[3 * LK_VS] << 16);
+                // halves d of the four rows, paired into two dwords
+                const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t v01 = __builtin_amdgcn_perm(d < 2 ? r[1].x : r[1].y, d < 2 ? r[0].x : r[0].y, sel);
+                const uint32_t v23 = __builtin_amdgcn_perm(d < 2 ? r[3].x : r[3].y, d < 2 ? r[2].x : r[2].y, sel);
                 const lk_h4 vb = h4_bits(v01, v23);
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[t], vb, o[d], 0, 0, 0);
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[t], vb, o[d], 0, 0, 0);
             }
         }
     }
-    // o[d] lane: heads 4j + i, dim 16d + c16 (relative to this wave's max)
+    // o[d] lane: heads 4j + i, dim 4 c16 + d (relative to this wave's max)
     __syncthreads();  // every wave is done with its V tile
     if (j == 0) {
         red_m[w][c16] = mt;  // -inf for a wave with no live tile
@@ -365,7 +375,7 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][16 * d + c16] = o[d][i];
+        for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][4 * c16 + d] = o[d][i];
     __syncthreads();
 
     // ---- merge the 4 tiles into one partial per query head
