@@ -41,8 +41,13 @@
 #define FT (FW * 64)
 #define FCH 64
 #define LKF_TRACE_MAX 256
-#define LKF_KB 3  // gate/up units per wave of half 1, issued in S1
-#define LKF_KA 2  // gate/up units per wave of half 0, issued in S4
+// gate/up units per wave of half 1 (issued in S1) and of half 0 (issued in
+// S4); the rest are issued and used in S5.  Q4_K rows carry their 16-byte
+// super-block heads: holding 3 + 2 of them spilled registers, and a spill
+// reload waits for every load in flight (TinyLlama shape: 1226 tok/s at
+// 3 + 2, 1493 at 1 + 1).
+#define LKF_KB (WT == LK_Q4_K ? 1 : 3)
+#define LKF_KA (WT == LK_Q4_K ? 1 : 2)
 // Stage timestamps of the traced block (thread 0), kept in LDS and copied
 // out at the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
