@@ -42,12 +42,14 @@
 #define FCH 64
 #define LKF_TRACE_MAX 256
 // gate/up units per wave of half 1 (issued in S1) and of half 0 (issued in
-// S4); the rest are issued and used in S5.  Q4_K rows carry their 16-byte
-// super-block heads: holding 3 + 2 of them spilled registers, and a spill
-// reload waits for every load in flight (TinyLlama shape: 1226 tok/s at
-// 3 + 2, 1493 at 1 + 1).
-#define LKF_KB (WT == LK_Q4_K ? 1 : 3)
-#define LKF_KA (WT == LK_Q4_K ? 1 : 2)
+// S4); the rest are issued and used in S5.  Measured per type: holding more
+// rows ahead raises register pressure (Q4_K rows carry 16-byte super-block
+// heads and spilled at 3 + 2; a spill reload waits for every load in
+// flight), holding fewer serialises S5.  Qwen2.5 Q8_0: 2 + 2 (2265 tok/s;
+// 3 + 2: 2217, 1 + 1: 2197); SmolLM2 F16: 1 + 1 (2207; 3 + 2: 2071);
+// TinyLlama Q4_K: 1 + 1 (1493; 3 + 2: 1226).
+#define LKF_KB (WT == LK_Q8_0 ? 2 : 1)
+#define LKF_KA (WT == LK_Q8_0 ? 2 : 1)
 // Stage timestamps of the traced block (thread 0), kept in LDS and copied
 // out at the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
@@ -376,6 +378,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         auto unit_of = [&](int k) -> int {
             return half1 ? (c.gw - nwh) + k * nwh : LKF_KB * nwh + c.gw + k * nwh;
         };
+        static_assert(LKF_KA <= LKF_KB, "half 0's units are held in the same registers as half 1's");
         const int nunits = half1 ? LKF_KB : LKF_KA;
         Row<WT, NCHH> orow;                 // issued in S1, used in S4
         Row<WT, NCHH> gq[LKF_KB], uq[LKF_KB];  // issued in S1 (half 1) or S4 (half 0), used in S5
