@@ -1049,6 +1049,27 @@ static hipError_t rows_gemm(Rows& R, LkGemmArgs a, int mode, hipStream_t st) {
 
 // One pass over n rows whose meta is already on the device; logits of the
 // last row (HEAD_LAST) or of every row (HEAD_ALL, n <= LK_ROWS_LOGITS).
+// The final RMSNorm (with `pend` split-K partials still to add to x) and the
+// lm_head GEMM of every row (HEAD_ALL) or of the last one (HEAD_LAST).
+static hipError_t enqueue_rows_head(const lkhip_engine* e, Rows& R, uint32_t n, const float* part, uint32_t pend,
+                                    int head, hipStream_t st) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t h = c.hidden_size;
+    float *x = R.x.as<float>(), *xn = R.xn.as<float>();
+    hipError_t err = lk_rows_accnorm_launch(x, part, pend, n, h, e->norm.as<float>(), c.rms_norm_eps, xn, st);
+    if (err != hipSuccess) return err;
+    LkGemmArgs a{};
+    a.nseg = 1;
+    a.seg[0] = {e->lm_head->dw, nullptr, R.logits.as<float>()};
+    a.N = c.vocab_size;
+    a.K = h;
+    a.n_rows = head == HEAD_ALL ? n : 1;
+    a.x = head == HEAD_ALL ? xn : xn + (size_t)(n - 1) * h;
+    a.ldx = h;
+    a.ldy = c.vocab_size;
+    return rows_gemm(R, a, LK_MV_STORE, st);
+}
+
 static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const KvDesc& kv, int head,
                                hipStream_t st) {
     const lkhip_config& c = e->cfg;
@@ -1169,20 +1190,7 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             RSTEP(lk_gemm_launch(a, LK_MV_ACC, st, &pend));
         }
     }
-    if (head != HEAD_NONE) {
-        const uint32_t hr = head == HEAD_ALL ? n : 1;
-        RSTEP(lk_rows_accnorm_launch(x, part, pend, n, h, e->norm.as<float>(), c.rms_norm_eps, xn, st));
-        LkGemmArgs a{};
-        a.nseg = 1;
-        a.seg[0] = {e->lm_head->dw, nullptr, R.logits.as<float>()};
-        a.N = c.vocab_size;
-        a.K = h;
-        a.n_rows = hr;
-        a.x = head == HEAD_ALL ? xn : xn + (size_t)(n - 1) * h;
-        a.ldx = h;
-        a.ldy = c.vocab_size;
-        RSTEP(rows_gemm(R, a, LK_MV_STORE, st));
-    }
+    if (head != HEAD_NONE) RSTEP(enqueue_rows_head(e, R, n, part, pend, head, st));
 #undef RSTEP
     return hipSuccess;
 }
@@ -1330,11 +1338,25 @@ struct lkhip_batch {
     Rows rows;
     std::vector<hipGraphExec_t> step_graph;    // by row count: logits of every row
     std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
+    // the multi-row one-kernel step (fused_rows.hip) for up to LK_FUSED_ROWS rows
+    bool fused_ok = false;
+    size_t fused_lds = 0;
+    uint32_t fused_chunks = 0;
+    DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
+    std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
+    void drop_fused_graphs() {
+        for (auto& v : fused_graph) {
+            for (auto g : v)
+                if (g) (void)hipGraphExecDestroy(g);
+            v.clear();
+        }
+    }
     ~lkhip_batch() {
         for (auto g : step_graph)
             if (g) (void)hipGraphExecDestroy(g);
         for (auto g : greedy_graph)
             if (g) (void)hipGraphExecDestroy(g);
+        drop_fused_graphs();
         if (stream) (void)hipStreamSynchronize(stream);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -1345,12 +1367,67 @@ static bool graphs_on() {
     return !(g && g[0] == '0');
 }
 
+// The multi-row one-kernel step over the rows whose meta is on the device,
+// leaving the final x rows in rows.x.
+static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st) {
+    const lkhip_engine* e = b->e;
+    const lkhip_config& c = e->cfg;
+    LkFusedArgs a{};
+    a.layers = e->fused_layers.as<LkFusedLayer>();
+    a.n_layers = c.num_hidden_layers;
+    a.embed = e->embed->dw;
+    a.norm = e->norm.as<float>();
+    a.freq = e->freq;
+    a.h = c.hidden_size;
+    a.I = c.intermediate_size;
+    a.nh = c.num_attention_heads;
+    a.nkv = c.num_key_value_heads;
+    a.vocab = c.vocab_size;
+    a.eps = c.rms_norm_eps;
+    a.kc = b->kv.kc;
+    a.vc = b->kv.vc;
+    a.kv_layer = b->kv.layer_bytes / 2;
+    a.max_seq = b->kv.kv_seq;
+    a.max_chunks = b->fused_chunks;
+    a.epoch = b->fepoch.as<uint32_t>();
+    a.err = b->ferr.as<uint32_t>();
+    a.xb = b->fxb.as<uint64_t>();
+    a.qb = b->fqb.as<uint64_t>();
+    a.pb = b->fpb.as<uint64_t>();
+    a.ab = b->fab.as<uint64_t>();
+    a.xpb = b->fxpb.as<uint64_t>();
+    a.ib = b->fib.as<uint64_t>();
+    a.meta = b->rows.meta.as<uint32_t>();
+    a.meta_cap = b->rows.cap;
+    a.nrows = n;
+    a.slot_elems = b->kv.slot_elems;
+    a.x_out = b->rows.x.as<float>();
+    return lk_fused_rows_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, e->fused_blocks,
+                                b->fused_lds, st, false);
+}
+
+// Whether the one-kernel step takes rows at these positions (the largest of
+// each row over the call): one wave per (row, head, 64-position tile).
+static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
+    if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS) return false;
+    const lkhip_config& c = b->e->cfg;
+    size_t items = (LK_FUSED_ROWS - last_pos.size()) * c.num_attention_heads;  // padding rows
+    for (size_t p : last_pos) {
+        if (p / 64 + 1 > b->fused_chunks) return false;
+        items += (size_t)c.num_attention_heads * (p / 64 + 1);
+    }
+    return items <= (size_t)b->e->fused_blocks * (lk_fused_threads() / 64);
+}
+
 // Enqueues a decode step of n rows (meta on the device); greedy adds the
-// argmax feedback.  Replays a captured graph when graphs are on.
-static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy) {
-    std::vector<hipGraphExec_t>& cache = greedy ? b->greedy_graph : b->step_graph;
+// argmax feedback.  Replays a captured graph when graphs are on.  fused: the
+// multi-row one-kernel step instead of the per-layer launches.
+static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, bool fused = false) {
+    std::vector<hipGraphExec_t>& cache =
+        fused ? b->fused_graph[greedy ? 1 : 0] : (greedy ? b->greedy_graph : b->step_graph);
     auto body = [&](hipStream_t st) -> hipError_t {
-        hipError_t err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        hipError_t err = fused ? batch_enqueue_fused(b, n, st) : enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        if (err == hipSuccess && fused) err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;
         return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
                                       b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
@@ -1409,8 +1486,48 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
     b->kv.kv_f32 = 0;
     const uint32_t cap = (uint32_t)std::max<size_t>(n_slots, std::min<size_t>(max_seq, LK_PREFILL_CHUNK));
     if ((rc = rows_alloc(e, b->rows, cap, (uint32_t)kv_seq))) return rc;
+    // the multi-row one-kernel step, where the model's shape has one
+    // (LKHIP_BATCH_FUSED=0 keeps every step on the per-layer launches)
+    const char* fe = getenv("LKHIP_BATCH_FUSED");
+    if (e->fused_ok && !(fe && fe[0] == '0') && kv_seq <= LK_FUSED_MAX_SEQ) {
+        const size_t h = c.hidden_size, I = c.intermediate_size, nb = LK_FUSED_ROWS;
+        const size_t qkvd = e->qd + 2 * e->kvd;
+        b->fused_chunks = (uint32_t)(kv_seq / 64);
+        b->fused_lds = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, nb);
+        LkFusedArgs probe{};
+        if (lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g,
+                                 e->fused_blocks, b->fused_lds, nullptr, true) == hipSuccess) {
+            if ((rc = dev_alloc(b->fxb, 2 * nb * h * 8)) || (rc = dev_alloc(b->fqb, 2 * nb * qkvd * 8)) ||
+                (rc = dev_alloc(b->fpb, 2 * nb * c.num_attention_heads * b->fused_chunks * 66 * 8)) ||
+                (rc = dev_alloc(b->fab, 2 * nb * e->qd * 8)) || (rc = dev_alloc(b->fxpb, 2 * nb * h * 8)) ||
+                (rc = dev_alloc(b->fib, 2 * nb * I * 8)) || (rc = dev_alloc(b->fepoch, 4)) ||
+                (rc = dev_alloc(b->ferr, 4)))
+                return rc;
+            const uint32_t one = 1;
+            HIP_OR_FAIL(hipMemcpy(b->fepoch.p, &one, 4, hipMemcpyHostToDevice));
+            b->fused_ok = true;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
     *out = b.release();
     return LKHIP_OK;
+}
+
+// Waits for the batch stream; if a bounded wait inside the multi-row
+// one-kernel step timed out, the batcher drops to the per-layer launches and
+// the call fails (repeating it recomputes the same positions).
+static int batch_sync_check(lkhip_batch* b, bool fused) {
+    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
+    if (!fused) return LKHIP_OK;
+    uint32_t flag = 0;
+    HIP_OR_FAIL(hipMemcpy(&flag, b->ferr.p, 4, hipMemcpyDeviceToHost));
+    if (!flag) return LKHIP_OK;
+    HIP_OR_FAIL(hipMemset(b->ferr.p, 0, 4));
+    b->fused_ok = false;
+    b->drop_fused_graphs();
+    return fail(LKHIP_E_HIP, "the multi-row one-kernel step timed out waiting on another workgroup (is every CU "
+                             "free?) — this batcher now runs the per-layer kernels; repeat the call");
 }
 extern "C" void lkhip_batch_destroy(lkhip_batch* b) { delete b; }
 
@@ -1461,13 +1578,17 @@ extern "C" int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, si
     int rc = batch_check_rows(b, rows, n_rows, 0);
     if (rc) return rc;
     const size_t V = b->e->cfg.vocab_size;
+    bool any_fused = false;
     for (size_t off = 0; off < n_rows; off += LK_ROWS_LOGITS) {  // logits of up to 64 rows per pass
         const uint32_t m = (uint32_t)std::min<size_t>(LK_ROWS_LOGITS, n_rows - off);
-        if ((rc = batch_upload_rows(b, rows + off, m)) || (rc = batch_enqueue_step(b, m, false))) return rc;
+        std::vector<size_t> last(m);
+        for (uint32_t i = 0; i < m; i++) last[i] = (size_t)rows[off + i].pos;
+        const bool fused = batch_fused_fits(b, last);
+        any_fused |= fused;
+        if ((rc = batch_upload_rows(b, rows + off, m)) || (rc = batch_enqueue_step(b, m, false, fused))) return rc;
         HIP_OR_FAIL(hipMemcpyAsync(logits_out + off * V, b->rows.logits.p, m * V * 4, hipMemcpyDeviceToHost, b->stream));
     }
-    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
-    return LKHIP_OK;
+    return batch_sync_check(b, any_fused);
 }
 
 extern "C" int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, size_t n_steps,
@@ -1488,16 +1609,23 @@ extern "C" int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, 
                 (void)hipGraphExecDestroy(g);
                 g = nullptr;
             }
+        for (auto& g : b->fused_graph[1])
+            if (g) {
+                (void)hipGraphExecDestroy(g);
+                g = nullptr;
+            }
         b->rows.out_ids = DevBuf();
         if ((rc = dev_alloc(b->rows.out_ids, need * 4))) return rc;
         b->rows.out_ids_cap = need;
     }
+    std::vector<size_t> last(n);
+    for (uint32_t i = 0; i < n; i++) last[i] = (size_t)rows[i].pos + n_steps - 1;
+    const bool fused = batch_fused_fits(b, last);
     if ((rc = batch_upload_rows(b, rows, n))) return rc;
     for (size_t s = 0; s < n_steps; s++)
-        if ((rc = batch_enqueue_step(b, n, true))) return rc;
+        if ((rc = batch_enqueue_step(b, n, true, fused))) return rc;
     HIP_OR_FAIL(hipMemcpyAsync(ids_out, b->rows.out_ids.p, need * 4, hipMemcpyDeviceToHost, b->stream));
-    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
-    return LKHIP_OK;
+    return batch_sync_check(b, fused);
 }
 
 // ------------------------------------------------------------------ memory

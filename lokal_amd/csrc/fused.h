@@ -39,6 +39,13 @@ struct LkFusedArgs {
     // L, then at the end of the block
     uint64_t* trace;
     uint32_t trace_block;
+    // Batcher rows (fused_rows.hip only): meta = u32 [ids | pos | slots | ...],
+    // meta_cap apart; nrows live rows; slot_elems = KV elements between two
+    // slots; x_out = the final layer's f32 rows [nrows][h]
+    const uint32_t* meta;
+    uint32_t meta_cap, nrows;
+    uint64_t slot_elems;
+    float* x_out;
 };
 // ... followed by 8 sub-steps of layer 1's attention stage (when the traced
 // block runs an attention unit there).
@@ -57,6 +64,12 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_WAVES 8u
 
 int lk_fused_threads();
+// The multi-row one-kernel step (fused_rows.hip): LK_FUSED_ROWS Batcher rows
+// per launch (fewer are padded), f16 KV.
+#define LK_FUSED_ROWS 4u
+size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb);
+hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, unsigned blocks,
+                                size_t lds, hipStream_t st, bool setup);
 // setup=true checks the shape is instantiated, sets the LDS limit and checks
 // one block fits per CU; setup=false launches `blocks` blocks.
 hipError_t lk_fused_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, int kv_f32, unsigned blocks,

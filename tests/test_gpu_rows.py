@@ -173,8 +173,20 @@ def test_forward_batch_matches_oracle_per_position(kind):
     om.close()
 
 
+# The Batcher's two device paths: the multi-row one-kernel step (fused_rows.hip,
+# up to 4 rows, where the model's shape has one) and the per-layer launches.
+BATCH_PATHS = ["fused", "layers"]
+
+
+@pytest.fixture
+def batch_path(request, monkeypatch):
+    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1" if request.param == "fused" else "0")
+    return request.param
+
+
+@pytest.mark.parametrize("batch_path", BATCH_PATHS, indirect=True)
 @pytest.mark.parametrize("kind", list(KINDS))
-def test_batcher_decode_step_matches_independent_sequences(kind):
+def test_batcher_decode_step_matches_independent_sequences(kind, batch_path):
     """Rows of different slots, lengths and positions in one step: each row's
     logits equal the oracle's for its own sequence (src/engine.rs:42-47)."""
     cfg, eng, om = build(kind, seed=5)
@@ -198,7 +210,8 @@ def test_batcher_decode_step_matches_independent_sequences(kind):
     om.close()
 
 
-def test_batcher_greedy_matches_per_sequence_greedy():
+@pytest.mark.parametrize("batch_path", BATCH_PATHS, indirect=True)
+def test_batcher_greedy_matches_per_sequence_greedy(batch_path):
     """lkhip_batch_decode_greedy: every row's ids equal that sequence's own
     greedy ids from a per-sequence decode_step loop with host argmax, and the
     oracle's ids up to a near-tie within tolerance."""
@@ -254,6 +267,45 @@ def test_batcher_refusals():
         bat.decode_greedy([BatchRow(1, 10, 0)], 8)
     with pytest.raises(LokalHipError, match="outside the vocabulary"):
         bat.prefill(0, np.array([cfg.vocab_size], np.uint32))
+    bat.close()
+    eng.close()
+    om.close()
+
+
+@pytest.mark.parametrize("kind", ["q8_0", "f16"])
+@pytest.mark.parametrize("n_rows", [1, 2, 3, 4])
+def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
+    """The multi-row one-kernel step at 1-4 rows (fewer than 4 are padded), on
+    slots other than 0..n-1: every row against the oracle over steps that
+    cross a 64-position tile, then greedy ids against the oracle's."""
+    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
+    cfg, eng, om = build(kind, seed=10 + n_rows)
+    rng = np.random.default_rng(n_rows)
+    lens = [60, 3, 127, 64][:n_rows]
+    slots = [i + 4 - n_rows for i in range(n_rows)]
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    bat = eng.batcher(4, 192)
+    orc = [om.session(192, kv_f16=True) for _ in lens]
+    for i, p in enumerate(prompts):
+        bat.prefill(slots[i], p)
+        orc[i].prefill(p)
+    pos = list(lens)
+    for step in range(6):
+        toks = [int(rng.integers(0, cfg.vocab_size)) for _ in lens]
+        outs = bat.decode_step([BatchRow(toks[i], pos[i], slots[i]) for i in range(n_rows)])
+        for i in range(n_rows):
+            assert rel_err(outs[i], orc[i].forward(toks[i], pos[i])) < TOL_F16_KV, (step, i)
+            pos[i] += 1
+    first = [int(rng.integers(0, cfg.vocab_size)) for _ in lens]
+    ids = bat.decode_greedy([BatchRow(first[i], pos[i], slots[i]) for i in range(n_rows)], 12)
+    for i in range(n_rows):
+        t, want = first[i], []
+        for k in range(12):
+            t = int(oracle.argmax(orc[i].forward(t, pos[i] + k)))
+            want.append(t)
+        agree = next((k for k in range(12) if ids[k, i] != want[k]), 12)
+        print(f"{kind} rows={n_rows} row {i}: {agree}/12 greedy ids agree with the CPU path")
+        assert agree >= 6
     bat.close()
     eng.close()
     om.close()
