@@ -92,7 +92,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         uint32_t* dst = (uint32_t*)lay;
         const uint32_t n32 = a.n_layers * (uint32_t)(sizeof(LkFusedLayer) / 4);
         for (uint32_t i = threadIdx.x; i < n32; i += FT) dst[i] = src[i];
-        __syncthreads();
+        lds_barrier();
     }
 
     Ctx c{&a, a.err, lane, wave, (int)(wave * gridDim.x + blockIdx.x), (int)(FW * gridDim.x)};
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     LKF_MARK(0);
     // S0: every block takes the embedding row itself (src/model.rs:200-202).
     for (uint32_t j = threadIdx.x; j < h; j += FT) xres[j] = lk_embed_elem(a.embed, token, j);
-    __syncthreads();
+    lds_barrier();
     LKF_MARK(1);
 
     for (uint32_t L = 0; L < nL; L++) {

@@ -21,6 +21,21 @@ struct Ctx {
     int lane, wave, gw, nw;
 };
 
+// Block barrier for data exchanged through LDS only.  __syncthreads() is
+// also a workgroup-scope release/acquire fence, and on this target that
+// waits for every global store still in flight (vmcnt(0)): after a stage
+// publishes its (value | epoch) words that is a full memory round trip per
+// barrier, paid by every wave.  The exchange words need no such ordering
+// (the epoch in each word is the completion flag), so the barrier waits for
+// this wave's LDS operations only; the empty asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt not waited
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ uint64_t word(float v, uint32_t ep) {
     return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
 }
@@ -98,7 +113,7 @@ __device__ __forceinline__ void awaitN(const Ctx& c, const uint64_t* src, uint32
 template <int N>
 __device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint32_t n, uint32_t ep, float* dst,
                                          int half) {
-    __syncthreads();  // every wave is done reading dst from the previous stage
+    lds_barrier();  // every wave is done reading dst from the previous stage
     if (half < 0) {
         for (uint32_t i = threadIdx.x; i < n; i += N * FT) awaitN<N>(c, src, i, FT, n, ep, dst);
     } else {
@@ -106,17 +121,17 @@ __device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint
         if ((int)(threadIdx.x >= FT / 2) == half)
             for (uint32_t i = t; i < n; i += N * (FT / 2)) awaitN<N>(c, src, i, FT / 2, n, ep, dst);
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = lk_wave_sum(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     float t = 0.f;
 #pragma unroll
     for (int i = 0; i < FW; i++) t += red[i];
-    __syncthreads();
+    lds_barrier();
     return t;
 }
 
@@ -128,7 +143,7 @@ __device__ __forceinline__ void rmsnorm_lds(const float* xr, const float* g, uin
     const float tot = block_sum(ss, red);
     const float scale = 1.0f / sqrtf(tot / (float)n + eps);
     for (uint32_t i = threadIdx.x; i < n; i += FT) xo[i] = __fmul_rn(__fmul_rn(xr[i], scale), g[i]);
-    __syncthreads();
+    lds_barrier();
 }
 
 __device__ __forceinline__ float kv_round(float v, bool f32) {

@@ -23,38 +23,62 @@
 // Exchange buffers are (f32 | epoch) words laid out [2 by layer parity][NB][..].
 #include "fused_impl.h"
 
-#define LKR_KB 1  // gate/up units per wave of half 1, issued in S1
-#define LKR_KA 1  // gate/up units per wave of half 0, issued in S4
+// gate/up units per wave of half 1 (issued after S2) and of half 0 (issued
+// in S4); the rest are issued and used in S5, which exposes a load latency
+#ifndef LKR_KB_F16
+#define LKR_KB_F16 2
+#define LKR_KA_F16 2
+#endif
+#define LKR_KB (WT == LK_F16 ? LKR_KB_F16 : 3)
+#define LKR_KA (WT == LK_F16 ? LKR_KA_F16 : 2)
 
 namespace lkf {
 
 using namespace lk;
 
 // math::rmsnorm (src/math.rs:45-49) of NB rows of n in LDS (row b at xr + b*n)
-// into xo; red holds NB * FW partial sums.
+// into xo; red holds NB * FW partial sums.  A thread's elements of every row
+// are read once into registers (one LDS round trip), squared and summed in
+// index order, then scaled from the same registers.
 template <int NB>
 __device__ __forceinline__ void rmsnorm_rows(const float* xr, const float* g, uint32_t n, float eps, float* xo,
                                              float* red) {
-    float ss[NB];
+    constexpr int EPT = ((int)LK_FUSED_MAX_H + FT - 1) / FT;
+    float v[NB][EPT], ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         ss[b] = 0.f;
-        for (uint32_t i = threadIdx.x; i < n; i += FT) ss[b] = fmaf(xr[b * n + i], xr[b * n + i], ss[b]);
-        ss[b] = lk_wave_sum(ss[b]);
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {
+            const uint32_t i = threadIdx.x + (uint32_t)e * FT;
+            v[b][e] = i < n ? xr[b * n + i] : 0.f;
+            ss[b] = fmaf(v[b][e], v[b][e], ss[b]);
+        }
     }
+#pragma unroll
+    for (int b = 0; b < NB; b++) ss[b] = lk_wave_sum(ss[b]);
     if ((threadIdx.x & 63) == 0)
 #pragma unroll
         for (int b = 0; b < NB; b++) red[b * FW + (threadIdx.x >> 6)] = ss[b];
-    __syncthreads();
+    lds_barrier();
+    float scale[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         float t = 0.f;
 #pragma unroll
         for (int i = 0; i < FW; i++) t += red[b * FW + i];
-        const float scale = 1.0f / sqrtf(t / (float)n + eps);
-        for (uint32_t i = threadIdx.x; i < n; i += FT) xo[b * n + i] = __fmul_rn(__fmul_rn(xr[b * n + i], scale), g[i]);
+        scale[b] = 1.0f / sqrtf(t / (float)n + eps);
     }
-    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+        const uint32_t i = threadIdx.x + (uint32_t)e * FT;
+        if (i < n) {
+            const float gv = g[i];
+#pragma unroll
+            for (int b = 0; b < NB; b++) xo[b * n + i] = __fmul_rn(__fmul_rn(v[b][e], scale[b]), gv);
+        }
+    }
+    lds_barrier();
 }
 
 template <int WT, int NCHH, int NCHI, int G, int NB>
@@ -81,7 +105,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
         uint32_t* dst = (uint32_t*)lay;
         const uint32_t n32 = a.n_layers * (uint32_t)(sizeof(LkFusedLayer) / 4);
         for (uint32_t i = threadIdx.x; i < n32; i += FT) dst[i] = src[i];
-        __syncthreads();
+        lds_barrier();
     }
 
     Ctx c{&a, a.err, lane, wave, (int)(wave * gridDim.x + blockIdx.x), (int)(FW * gridDim.x)};
@@ -99,6 +123,28 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
         posr[b] = __builtin_amdgcn_readfirstlane(live ? a.meta[a.meta_cap + b] : 0u);
         slotr[b] = __builtin_amdgcn_readfirstlane(a.meta[2 * a.meta_cap + (live ? b : 0)]);
     }
+    // the same in LDS for loops kept rolled (an indexed register array would
+    // live in scratch, and a scratch read waits for every load in flight)
+    __shared__ uint32_t rpos[NB], rslot[NB];
+    __shared__ float rcs[NB][32][2];  // RoPE (cos, sin) of pair ip at row b's position
+    if (threadIdx.x < NB) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if ((int)threadIdx.x == b) {
+                rpos[b] = posr[b];
+                rslot[b] = slotr[b];
+            }
+    }
+    if (threadIdx.x < NB * 32) {  // pos * theta^(-2 ip / 64)
+        const uint32_t b = threadIdx.x / 32, ipp = threadIdx.x % 32;
+        uint32_t pb = posr[0];
+#pragma unroll
+        for (int k = 1; k < NB; k++) pb = b == (uint32_t)k ? posr[k] : pb;
+        const float ang = __fmul_rn((float)pb, a.freq.f[ipp]);
+        rcs[b][ipp][0] = cosf(ang);
+        rcs[b][ipp][1] = sinf(ang);
+    }
+    // (visible after the barrier that ends the embedding stage)
     // attention items of row b: nh * ntile(b), one wave each
     uint32_t item0[NB + 1];
     item0[0] = 0;
@@ -126,19 +172,6 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
         row_issue(q2, w, head * 64 + ip + 32, lane);
     };
     if (has1) issue_qkv(lay[0]);
-    // RoPE angle of each row: pos * theta^(-2 ip / 64), in scalar registers
-    float rc[NB], rsn[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float cc = 1.f, ss = 0.f;
-        if (has1 && kind < 2) {
-            const float ang = __fmul_rn((float)posr[b], a.freq.f[ip]);
-            ss = sinf(ang);
-            cc = cosf(ang);
-        }
-        rc[b] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cc)));
-        rsn[b] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, ss)));
-    }
     for (uint32_t i = threadIdx.x; i < h; i += FT) {
         gin[i] = lk_g(lay[0].in_norm)[i];
         gpost[i] = lk_g(lay[0].post_norm)[i];
@@ -147,7 +180,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
 #pragma unroll
     for (int b = 0; b < NB; b++)
         for (uint32_t j = threadIdx.x; j < h; j += FT) xres[b * h + j] = lk_embed_elem(a.embed, tok[b], j);
-    __syncthreads();
+    lds_barrier();
 
     const uint16_t* kc0 = (const uint16_t*)a.kc;
     const uint16_t* vc0 = (const uint16_t*)a.vc;
@@ -182,16 +215,23 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
         }
         if (L > 0) stage_in<16>(c, a.xb + (size_t)par * NB * h, NB * h, ep, xres, 1);
         rmsnorm_rows<NB>(xres, gin, h, a.eps, xin, red);
+        // the row loops below stay rolled: unrolled, every row's LDS
+        // addresses stay live and spill
         if (has1) {
+            float d1r[NB], d2r[NB];  // every row's dots first: their LDS reads overlap
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                float d1 = lk_wave_sum(row_dot(q1, xin + b * h, h, lane));
-                float d2 = lk_wave_sum(row_dot(q2, xin + b * h, h, lane));
+                d1r[b] = lk_wave_sum(row_dot(q1, xin + b * h, h, lane));
+                d2r[b] = lk_wave_sum(row_dot(q2, xin + b * h, h, lane));
+            }
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                float d1 = d1r[b], d2 = d2r[b];
                 if (lane == 0) {
                     const uint32_t r = head * 64 + ip;
                     d1 += b1;
                     d2 += b2;
-                    if (kind < 2) rot(d1, d2, rc[b], rsn[b]);
+                    if (kind < 2) rot(d1, d2, rcs[b][ip][0], rcs[b][ip][1]);
                     uint64_t* qb = QB + (size_t)b * qkvd;
                     if (kind == 0) {
                         publish(qb + r, d1, ep);
@@ -199,8 +239,8 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                     } else {
                         if ((uint32_t)b < nrows) {
                             uint16_t* cache = (uint16_t*)(kind == 1 ? a.kc : a.vc) + lay_off +
-                                              (size_t)slotr[b] * a.slot_elems +
-                                              ((size_t)head * a.max_seq + posr[b]) * 64;
+                                              (size_t)rslot[b] * a.slot_elems +
+                                              ((size_t)head * a.max_seq + rpos[b]) * 64;
                             kv_put(cache + ip, d1);
                             kv_put(cache + ip + 32, d2);
                         }
@@ -240,17 +280,6 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
             for (int q = 0; q < KC; q++) kraw[q] = *(const lk_u32x4*)((const uint8_t*)Kl + 16 * q);
 #pragma unroll
             for (int q = 0; q < KC; q++) vraw[q] = *(const lk_u32x4*)(Vl + q * 8 * 64);
-        }
-        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
-        if (half1) {
-#pragma unroll
-            for (int k = 0; k < LKR_KB; k++) {
-                const int uu = unit_of(k);
-                if (uu < (int)I) {
-                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
-                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
-                }
-            }
         }
         // ---------------- S2: attention partials (as fused.hip, per row)
         if (has2) {
@@ -348,6 +377,20 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                 for (int e = 0; e < 8; e++) publish(out + 2 + dq + e, acc[e], ep);
             }
         }
+        // o_proj rows (and half 1's gate/up rows) are issued after the
+        // attention stage: held across it they would push its K/V tile out of
+        // registers
+        if (c.gw < (int)h) row_issue(orow, ly.o, (uint32_t)c.gw, lane);
+        if (half1) {
+#pragma unroll
+            for (int k = 0; k < LKR_KB; k++) {
+                const int uu = unit_of(k);
+                if (uu < (int)I) {
+                    row_issue(gq[k], ly.gate, (uint32_t)uu, lane);
+                    row_issue(uq[k], ly.up, (uint32_t)uu, lane);
+                }
+            }
+        }
         // ---------------- S3: merge each (row, head)'s tiles -> attention output (lane = dim)
         if (c.gw < (int)(NB * nh)) {
             const uint32_t b3 = (uint32_t)c.gw / nh, h3 = (uint32_t)c.gw % nh;
@@ -409,7 +452,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
         {
             stage_in<8>(c, AB, NB * qd, ep, xin, -1);
             if (c.gw < (int)h) {
-#pragma unroll
+#pragma unroll 1
                 for (int b = 0; b < NB; b++) {
                     const float d = lk_wave_sum(row_dot(orow, xin + b * qd, qd, lane));
                     if (lane == 0) publish(XP + (size_t)b * h + c.gw, xres[b * h + c.gw] + d, ep);
@@ -434,7 +477,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
             for (int k = 0; k < LKR_KB; k++) {
                 const int uu = unit_of(k);
                 if (k < nunits && uu < (int)I) {
-#pragma unroll
+#pragma unroll 1
                     for (int b = 0; b < NB; b++) {
                         const float gg = lk_wave_sum(row_dot(gq[k], xin + b * h, h, lane));
                         const float up = lk_wave_sum(row_dot(uq[k], xin + b * h, h, lane));
@@ -446,7 +489,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                 Row<WT, NCHH> gr, pr;
                 row_issue(gr, ly.gate, (uint32_t)uu, lane);
                 row_issue(pr, ly.up, (uint32_t)uu, lane);
-#pragma unroll
+#pragma unroll 1
                 for (int b = 0; b < NB; b++) {
                     const float gg = lk_wave_sum(row_dot(gr, xin + b * h, h, lane));
                     const float up = lk_wave_sum(row_dot(pr, xin + b * h, h, lane));
@@ -467,7 +510,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                 else if ((uint32_t)b < nrows) a.x_out[(size_t)b * h + u] = v;
             };
             if (c.gw < (int)h) {
-#pragma unroll
+#pragma unroll 1
                 for (int b = 0; b < NB; b++) {
                     const float d = lk_wave_sum(row_dot(dn, xin + b * I, I, lane));
                     if (lane == 0) put(b, c.gw, xres[b * h + c.gw] + d);
@@ -476,7 +519,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
             for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
                 Row<WT, NCHI> rr;
                 row_issue(rr, ly.down, (uint32_t)uu, lane);
-#pragma unroll
+#pragma unroll 1
                 for (int b = 0; b < NB; b++) {
                     const float d = lk_wave_sum(row_dot(rr, xin + b * I, I, lane));
                     if (lane == 0) put(b, uu, xres[b * h + uu] + d);
