@@ -36,51 +36,6 @@ namespace lkf {
 
 using namespace lk;
 
-// math::rmsnorm (src/math.rs:45-49) of NB rows of n in LDS (row b at xr + b*n)
-// into xo; red holds NB * FW partial sums.  A thread's elements of every row
-// are read once into registers (one LDS round trip), squared and summed in
-// index order, then scaled from the same registers.
-template <int NB>
-__device__ __forceinline__ void rmsnorm_rows(const float* xr, const float* g, uint32_t n, float eps, float* xo,
-                                             float* red) {
-    constexpr int EPT = ((int)LK_FUSED_MAX_H + FT - 1) / FT;
-    float v[NB][EPT], ss[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        ss[b] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPT; e++) {
-            const uint32_t i = threadIdx.x + (uint32_t)e * FT;
-            v[b][e] = i < n ? xr[b * n + i] : 0.f;
-            ss[b] = fmaf(v[b][e], v[b][e], ss[b]);
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < NB; b++) ss[b] = lk_wave_sum(ss[b]);
-    if ((threadIdx.x & 63) == 0)
-#pragma unroll
-        for (int b = 0; b < NB; b++) red[b * FW + (threadIdx.x >> 6)] = ss[b];
-    lds_barrier();
-    float scale[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float t = 0.f;
-#pragma unroll
-        for (int i = 0; i < FW; i++) t += red[b * FW + i];
-        scale[b] = 1.0f / sqrtf(t / (float)n + eps);
-    }
-#pragma unroll
-    for (int e = 0; e < EPT; e++) {
-        const uint32_t i = threadIdx.x + (uint32_t)e * FT;
-        if (i < n) {
-            const float gv = g[i];
-#pragma unroll
-            for (int b = 0; b < NB; b++) xo[b * n + i] = __fmul_rn(__fmul_rn(v[b][e], scale[b]), gv);
-        }
-    }
-    lds_barrier();
-}
-
 template <int WT, int NCHH, int NCHI, int G, int NB>
 __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) {
     extern __shared__ float lds[];
