@@ -1340,7 +1340,7 @@ struct lkhip_batch {
     std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
     // the multi-row one-kernel step (fused_rows.hip) for up to LK_FUSED_ROWS rows
     bool fused_ok = false;
-    size_t fused_lds = 0;
+    size_t fused_lds[2] = {0, 0};  // 4-row and LK_FUSED_ROWS-row kernels
     uint32_t fused_chunks = 0;
     DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
     std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
@@ -1402,8 +1402,9 @@ static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st
     a.nrows = n;
     a.slot_elems = b->kv.slot_elems;
     a.x_out = b->rows.x.as<float>();
-    return lk_fused_rows_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, e->fused_blocks,
-                                b->fused_lds, st, false);
+    const uint32_t nb = n <= 4 ? 4 : LK_FUSED_ROWS;
+    return lk_fused_rows_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, nb,
+                                e->fused_blocks, b->fused_lds[nb > 4], st, false);
 }
 
 // Whether the one-kernel step takes rows at these positions (the largest of
@@ -1411,7 +1412,8 @@ static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st
 static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
     if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS) return false;
     const lkhip_config& c = b->e->cfg;
-    size_t items = (LK_FUSED_ROWS - last_pos.size()) * c.num_attention_heads;  // padding rows
+    const size_t nb = last_pos.size() <= 4 ? 4 : LK_FUSED_ROWS;
+    size_t items = (nb - last_pos.size()) * c.num_attention_heads;  // padding rows
     for (size_t p : last_pos) {
         if (p / 64 + 1 > b->fused_chunks) return false;
         items += (size_t)c.num_attention_heads * (p / 64 + 1);
@@ -1493,10 +1495,15 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         const size_t h = c.hidden_size, I = c.intermediate_size, nb = LK_FUSED_ROWS;
         const size_t qkvd = e->qd + 2 * e->kvd;
         b->fused_chunks = (uint32_t)(kv_seq / 64);
-        b->fused_lds = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, nb);
         LkFusedArgs probe{};
-        if (lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g,
-                                 e->fused_blocks, b->fused_lds, nullptr, true) == hipSuccess) {
+        bool ok = true;
+        for (int k = 0; k < 2 && ok; k++) {
+            const uint32_t kb = k ? LK_FUSED_ROWS : 4;
+            b->fused_lds[k] = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, kb);
+            ok = lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, kb,
+                                      e->fused_blocks, b->fused_lds[k], nullptr, true) == hipSuccess;
+        }
+        if (ok) {
             if ((rc = dev_alloc(b->fxb, 2 * nb * h * 8)) || (rc = dev_alloc(b->fqb, 2 * nb * qkvd * 8)) ||
                 (rc = dev_alloc(b->fpb, 2 * nb * c.num_attention_heads * b->fused_chunks * 66 * 8)) ||
                 (rc = dev_alloc(b->fab, 2 * nb * e->qd * 8)) || (rc = dev_alloc(b->fxpb, 2 * nb * h * 8)) ||

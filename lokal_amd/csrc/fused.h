@@ -64,12 +64,12 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_WAVES 8u
 
 int lk_fused_threads();
-// The multi-row one-kernel step (fused_rows.hip): LK_FUSED_ROWS Batcher rows
-// per launch (fewer are padded), f16 KV.
-#define LK_FUSED_ROWS 4u
+// The multi-row one-kernel step (fused_rows.hip): 4 or LK_FUSED_ROWS Batcher
+// rows per launch (fewer are padded), f16 KV.
+#define LK_FUSED_ROWS 8u
 size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb);
-hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, unsigned blocks,
-                                size_t lds, hipStream_t st, bool setup);
+hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, uint32_t nb,
+                                unsigned blocks, size_t lds, hipStream_t st, bool setup);
 // setup=true checks the shape is instantiated, sets the LDS limit and checks
 // one block fits per CU; setup=false launches `blocks` blocks.
 hipError_t lk_fused_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, int kv_f32, unsigned blocks,

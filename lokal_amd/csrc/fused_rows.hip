@@ -23,6 +23,8 @@
 // Exchange buffers are (f32 | epoch) words laid out [2 by layer parity][NB][..].
 #include "fused_impl.h"
 
+#include <algorithm>
+
 // gate/up units per wave of half 1 (issued after S2) and of half 0 (issued
 // in S4); the rest are issued and used in S5, which exposes a load latency
 #ifndef LKR_KB_F16
@@ -41,9 +43,12 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
     extern __shared__ float lds[];
     const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
-    const uint32_t vmax = (I > h ? I : h) > qd ? (I > h ? I : h) : qd;
-    float* xin = lds;                   // NB * vmax: the (normalised) input rows of a stage
-    float* xres = xin + NB * vmax;      // NB * h: the residual rows
+    // the down stage takes its input S6R rows at a time, so that NB = 8 fits
+    constexpr int S6R = NB < 4 ? NB : 4;
+    const uint32_t hq_max = h > qd ? h : qd;
+    const uint32_t xin_n = NB * hq_max > S6R * I ? NB * hq_max : S6R * I;
+    float* xin = lds;                   // xin_n: the (normalised) input rows of a stage
+    float* xres = xin + xin_n;          // NB * h: the residual rows
     float* red = xres + NB * h;         // NB * FW: block reductions
     float* gin = red + NB * FW;         // h
     float* gpost = gin + h;             // h
@@ -459,25 +464,28 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
             const uint32_t epn = ep + 1;
             uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * NB * h;
             const bool last = L + 1 == nL;
-            stage_in<24>(c, IB, NB * I, ep, xin, -1);
             auto put = [&](int b, int u, float v) {
                 if (!last) publish(XN + (size_t)b * h + u, v, epn);
                 else if ((uint32_t)b < nrows) a.x_out[(size_t)b * h + u] = v;
             };
-            if (c.gw < (int)h) {
 #pragma unroll 1
-                for (int b = 0; b < NB; b++) {
-                    const float d = lk_wave_sum(row_dot(dn, xin + b * I, I, lane));
-                    if (lane == 0) put(b, c.gw, xres[b * h + c.gw] + d);
+            for (int p0 = 0; p0 < NB; p0 += S6R) {  // S6R rows of the SwiGLU input at a time
+                stage_in<24>(c, IB + (size_t)p0 * I, S6R * I, ep, xin, -1);
+                if (c.gw < (int)h) {
+#pragma unroll 1
+                    for (int b = 0; b < S6R; b++) {
+                        const float d = lk_wave_sum(row_dot(dn, xin + b * I, I, lane));
+                        if (lane == 0) put(p0 + b, c.gw, xres[(p0 + b) * h + c.gw] + d);
+                    }
                 }
-            }
-            for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
-                Row<WT, NCHI> rr;
-                row_issue(rr, ly.down, (uint32_t)uu, lane);
+                for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
+                    Row<WT, NCHI> rr;
+                    row_issue(rr, ly.down, (uint32_t)uu, lane);
 #pragma unroll 1
-                for (int b = 0; b < NB; b++) {
-                    const float d = lk_wave_sum(row_dot(rr, xin + b * I, I, lane));
-                    if (lane == 0) put(b, uu, xres[b * h + uu] + d);
+                    for (int b = 0; b < S6R; b++) {
+                        const float d = lk_wave_sum(row_dot(rr, xin + b * I, I, lane));
+                        if (lane == 0) put(p0 + b, uu, xres[(p0 + b) * h + uu] + d);
+                    }
                 }
             }
             // the next layer's gains, by half 0 (half 1 polls first in S1);
@@ -497,9 +505,10 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
 }  // namespace lkf
 
 size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb) {
-    uint32_t vmax = I > h ? I : h;
-    if (nh * 64 > vmax) vmax = nh * 64;
-    return ((size_t)nb * vmax + (size_t)nb * h + (size_t)nb * FW + 2 * (size_t)h + (size_t)FW * 256) * 4 +
+    const size_t s6r = nb < 4 ? nb : 4;
+    const size_t hq_max = h > nh * 64 ? h : nh * 64;
+    const size_t xin_n = std::max((size_t)nb * hq_max, s6r * I);
+    return (xin_n + (size_t)nb * h + (size_t)nb * FW + 2 * (size_t)h + (size_t)FW * 256) * 4 +
            LK_FUSED_MAX_LAYERS * sizeof(LkFusedLayer);
 }
 
@@ -519,16 +528,17 @@ static hipError_t launch_rows_t(const LkFusedArgs& a, unsigned blocks, size_t ld
 }
 
 // Instantiated shapes: (weight type, 16-byte chunks per lane for rows of
-// hidden / intermediate width, GQA group), f16 KV, LK_FUSED_ROWS rows.
+// hidden / intermediate width, GQA group), f16 KV, 4 or LK_FUSED_ROWS rows.
 #define LKR_SHAPES(X)                       \
     X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */ \
     X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */
 
-hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, unsigned blocks,
-                                size_t lds, hipStream_t st, bool setup) {
-#define X(T, NH, NI, GG)                                                                   \
-    if (wt == T && nchh == NH && nchi == NI && G == GG)                                    \
-        return launch_rows_t<T, NH, NI, GG, LK_FUSED_ROWS>(a, blocks, lds, st, setup);
+hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, uint32_t nb,
+                                unsigned blocks, size_t lds, hipStream_t st, bool setup) {
+#define X(T, NH, NI, GG)                                                                           \
+    if (wt == T && nchh == NH && nchi == NI && G == GG)                                            \
+        return nb <= 4 ? launch_rows_t<T, NH, NI, GG, 4>(a, blocks, lds, st, setup)                \
+                       : launch_rows_t<T, NH, NI, GG, LK_FUSED_ROWS>(a, blocks, lds, st, setup);
     LKR_SHAPES(X)
 #undef X
     return hipErrorNotSupported;

@@ -273,18 +273,19 @@ def test_batcher_refusals():
 
 
 @pytest.mark.parametrize("kind", ["q8_0", "f16"])
-@pytest.mark.parametrize("n_rows", [1, 2, 3, 4])
+@pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 8])
 def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
-    """The multi-row one-kernel step at 1-4 rows (fewer than 4 are padded), on
-    slots other than 0..n-1: every row against the oracle over steps that
-    cross a 64-position tile, then greedy ids against the oracle's."""
+    """The multi-row one-kernel step at 1-8 rows (4- and 8-row kernels, fewer
+    rows padded), on slots other than 0..n-1: every row against the oracle
+    over steps that cross a 64-position tile, then greedy ids against the
+    oracle's."""
     monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
     cfg, eng, om = build(kind, seed=10 + n_rows)
     rng = np.random.default_rng(n_rows)
-    lens = [60, 3, 127, 64][:n_rows]
-    slots = [i + 4 - n_rows for i in range(n_rows)]
+    lens = [60, 3, 127, 64, 1, 100, 20, 63][:n_rows]
+    slots = [i + 8 - n_rows for i in range(n_rows)]
     prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
-    bat = eng.batcher(4, 192)
+    bat = eng.batcher(8, 192)
     orc = [om.session(192, kv_f16=True) for _ in lens]
     for i, p in enumerate(prompts):
         bat.prefill(slots[i], p)
