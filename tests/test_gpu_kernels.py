@@ -231,6 +231,15 @@ def test_attention_config5_four_sequences_32k():
     _attn_case(4, 14, 2, [32768, 32768, 16384, 4096], 32768, seed=7)
 
 
+def test_attention_merge_boundary_and_repeat():
+    """Contexts on both sides of 32 chunks (8192 positions: one fold round
+    per merge wave) in one call, repeated on the same cached partial buffer
+    with other shapes in between."""
+    for rep in range(3):
+        _attn_case(3, 14, 2, [8192, 8193, 8191], 8448, seed=21 + rep)
+        _attn_case(2, 14, 2, [8192, 256], 8192, seed=31 + rep)
+
+
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])
 def test_attention_both_f16_kernels(kernel, monkeypatch):
     """The vector-ALU and matrix-core partial kernels (the matrix-core one by
@@ -240,6 +249,7 @@ def test_attention_both_f16_kernels(kernel, monkeypatch):
     _attn_case(3, 9, 3, [300, 17, 1000], 1024, seed=12)
     _attn_case(4, 32, 4, [4096, 1, 2500, 777], 4096, seed=13)
     _attn_case(2, 14, 2, [16384, 9999], 16384, seed=14)
+    _attn_case(3, 14, 2, [8192, 8193, 8191], 8448, seed=15)
 
 
 def test_argmax_first_max_wins():
