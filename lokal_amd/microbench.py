@@ -21,7 +21,9 @@ Prints one JSON object per measurement:
   batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
           with a 512-token prompt, then 64 greedy steps of all B rows on the
           device: aggregate tok/s and weight GB/s (one weight read per step).
-Kernel times come from hipEvents around repeated launches on one stream.
+Kernel times come from hipEvents around repeated launches on one stream; the
+layer kernels are also timed as 200 launches captured in one HIP graph
+(us_graph: device time per launch without the per-call host cost).
 """
 from __future__ import annotations
 
@@ -50,6 +52,47 @@ def _timed(fn, reps: int, stream: K.Stream) -> float:
     b.record(stream)
     stream.synchronize()
     return a.elapsed_ms(b) / reps
+
+
+def _hip():
+    """The HIP runtime, for stream capture (measurement only)."""
+    import ctypes
+    h = ctypes.CDLL("libamdhip64.so")
+    for f in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+              "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(h, f).restype = ctypes.c_int
+    return h
+
+
+def _timed_graph(fn, reps: int, stream: K.Stream) -> float:
+    """Average ms per launch of fn() captured reps times into one HIP graph
+    (device time per kernel without the per-call host launch cost)."""
+    import ctypes
+    h = _hip()
+    fn()  # load the code object outside the capture
+    stream.synchronize()
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    if h.hipStreamBeginCapture(stream.ptr, 2):  # hipStreamCaptureModeRelaxed
+        raise RuntimeError("hipStreamBeginCapture failed")
+    for _ in range(reps):
+        fn()
+    if h.hipStreamEndCapture(stream.ptr, ctypes.byref(graph)):
+        raise RuntimeError("hipStreamEndCapture failed")
+    try:
+        if h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)):
+            raise RuntimeError("hipGraphInstantiate failed")
+        h.hipGraphLaunch(exe, stream.ptr)  # warm-up
+        a, b = K.Event(), K.Event()
+        a.record(stream)
+        if h.hipGraphLaunch(exe, stream.ptr):
+            raise RuntimeError("hipGraphLaunch failed")
+        b.record(stream)
+        stream.synchronize()
+        return a.elapsed_ms(b) / reps
+    finally:
+        if exe:
+            h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
 
 
 def decode(name: str, prompt_len: int, steps: int) -> dict:
@@ -84,28 +127,32 @@ def layers() -> list[dict]:
         x = K.DeviceArray.from_numpy(rng.standard_normal((rows, h)).astype(np.float32))
         g = K.DeviceArray.from_numpy((1 + 0.1 * rng.standard_normal(h)).astype(np.float32))
         y = K.DeviceArray((rows, h))
-        ms = _timed(lambda: K.rmsnorm(x, g, rows, h, 1e-6, y, st.ptr), 200, st)
+        f = lambda: K.rmsnorm(x, g, rows, h, 1e-6, y, st.ptr)
+        ms, gms = _timed(f, 200, st), _timed_graph(f, 200, st)
         nbytes = rows * h * 4 * 2 + h * 4
-        out.append({"kernel": "rmsnorm", "rows": rows, "n": h, "us": round(ms * 1e3, 3),
+        out.append({"kernel": "rmsnorm", "rows": rows, "n": h, "us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
         q = K.DeviceArray.from_numpy(rng.standard_normal((rows, nq * 64)).astype(np.float32))
         pos = K.DeviceArray.from_numpy(rng.integers(0, 32768, rows).astype(np.uint32))
-        ms = _timed(lambda: K.rope_pairs(q, rows, nq * 64, 64, pos, 1e6, st.ptr), 200, st)
+        f = lambda: K.rope_pairs(q, rows, nq * 64, 64, pos, 1e6, st.ptr)
+        ms, gms = _timed(f, 200, st), _timed_graph(f, 200, st)
         nbytes = rows * nq * 64 * 4 * 2 + rows * 4
-        out.append({"kernel": "rope_pairs", "rows": rows, "n": nq * 64, "us": round(ms * 1e3, 3),
+        out.append({"kernel": "rope_pairs", "rows": rows, "n": nq * 64, "us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
         gd = K.DeviceArray.from_numpy(rng.standard_normal(rows * inter).astype(np.float32))
         ud = K.DeviceArray.from_numpy(rng.standard_normal(rows * inter).astype(np.float32))
         od = K.DeviceArray(rows * inter)
-        ms = _timed(lambda: K.swiglu(gd, ud, rows * inter, od, st.ptr), 200, st)
+        f = lambda: K.swiglu(gd, ud, rows * inter, od, st.ptr)
+        ms, gms = _timed(f, 200, st), _timed_graph(f, 200, st)
         nbytes = rows * inter * 4 * 3
-        out.append({"kernel": "swiglu", "rows": rows, "n": inter, "us": round(ms * 1e3, 3),
+        out.append({"kernel": "swiglu", "rows": rows, "n": inter, "us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
         ids = K.DeviceArray.from_numpy(rng.integers(0, vocab, rows).astype(np.uint32))
         eo = K.DeviceArray((rows, h))
-        ms = _timed(lambda: K.embed_gather(table, ids, rows, eo, st.ptr), 200, st)
+        f = lambda: K.embed_gather(table, ids, rows, eo, st.ptr)
+        ms, gms = _timed(f, 200, st), _timed_graph(f, 200, st)
         nbytes = rows * h * (2 + 4) + rows * 4
-        out.append({"kernel": "embed_gather_f16", "rows": rows, "n": h, "us": round(ms * 1e3, 3),
+        out.append({"kernel": "embed_gather_f16", "rows": rows, "n": h, "us": round(ms * 1e3, 3), "us_graph": round(gms * 1e3, 3),
                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
     st.close()
     return out
