@@ -69,9 +69,37 @@ def copy_calibration(mb: int) -> None:
     check(lib().lkhip_free(dst))
 
 
+def host_cpus() -> dict:
+    """What this host gives the process: logical CPUs, the ones it may run on,
+    the cgroup CPU quota (cores' worth of time), and the CPU model."""
+    info = {"nproc": os.cpu_count() or 1, "affinity": len(os.sched_getaffinity(0)), "cgroup_quota": None,
+            "model": None}
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            info["cgroup_quota"] = round(int(q) / int(per), 2)
+    except (OSError, ValueError):
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                info["model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return info
+
+
 def cpu_baseline(cfg, tensors, prompt_len: int, budget_s: float) -> dict:
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    # the -O3 -mavx2 build of the oracle (bit-identical to the parity build)
+    # on every CPU this process may use; a cgroup quota below that caps the
+    # threads that can run at once, so the thread count follows the quota
+    oracle.select("o3")
+    hc = host_cpus()
+    threads = hc["affinity"]
+    if hc["cgroup_quota"]:
+        threads = max(1, min(threads, int(hc["cgroup_quota"])))
     oracle.set_threads(threads)
     om = oracle.Model(cfg, tensors)
     rng = np.random.default_rng(11)
@@ -95,6 +123,8 @@ def cpu_baseline(cfg, tensors, prompt_len: int, budget_s: float) -> dict:
     s.close()
     om.close()
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "nproc": hc["nproc"], "affinity_cpus": hc["affinity"], "cgroup_cpu_quota": hc["cgroup_quota"],
+            "cpu_model": hc["model"], "build": "gcc -O3 -mavx2 -fopenmp -ffp-contract=off (bit-identical to -O2)",
             "sample": f"{n} greedy decode tokens after a {prompt_len}-token prefill and 1 warm-up token, "
                       f"same synthetic Q8_0 weights expanded to f32 (lokal's load_f32 path), "
                       f"{threads} OpenMP threads, {dt:.1f} s"}

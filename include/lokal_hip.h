@@ -125,6 +125,14 @@ int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_tensor* ten
  * (src/gpu/metal.rs:1667); config from GGUF metadata as gguf::model_config does
  * (src/gguf/arch.rs:164-223). */
 int lkhip_engine_create_gguf(const char* path, lkhip_engine** out);
+/* The --context-window contract of the "hip" arm.  engine::create and
+ * create_metal_quant take win: Option<(window, sink)> (src/engine.rs:76-87,
+ * :150-162, built in src/main.rs:159-162); this backend keeps every position's
+ * K/V resident in HBM and has no sliding window, so, like the CPU arm
+ * (src/engine.rs:84-87), it refuses one: window == 0 (None) returns LKHIP_OK,
+ * any other value LKHIP_E_UNSUPPORTED with a one-line reason naming the
+ * backends that window.  No device needed. */
+int lkhip_context_window(size_t window, size_t sink);
 /* Parses a GGUF file's header and tensor table only (no device needed): the
  * config lkhip_engine_create_gguf would build (gguf::model_config,
  * src/gguf/arch.rs:164-227), the number of tensors the decode step reads

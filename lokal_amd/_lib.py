@@ -69,6 +69,7 @@ SIGNATURES = {
     "lkhip_engine_create_tensors": (C.c_int, [C.POINTER(Config), C.POINTER(TensorDesc), C.c_size_t, C.c_int,
                                               C.POINTER(_P)]),
     "lkhip_engine_create_gguf": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "lkhip_context_window": (C.c_int, [C.c_size_t, C.c_size_t]),
     "lkhip_gguf_config": (C.c_int, [C.c_char_p, C.POINTER(Config), C.POINTER(C.c_size_t), C.POINTER(C.c_int)]),
     "lkhip_engine_destroy": (None, [_P]),
     "lkhip_engine_config": (C.c_int, [_P, C.POINTER(Config)]),

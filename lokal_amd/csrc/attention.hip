@@ -30,6 +30,7 @@
 
 uint32_t lk_attn_chunk(uint32_t) { return LK_ACHUNK; }
 
+
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq) {
     const size_t nch = (max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
     return (size_t)n_seq * n_heads * nch * (2 + LK_HD);

@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -50,6 +51,47 @@ extern "C" int lkhip_device_count(void) {
         return 0;
     }
     return n;
+}
+
+
+// ------------------------------------------------- co-resident launch gate
+// The one-kernel steps (fused.hip, fused_rows.hip) and the lm_head launch
+// (lmhead.hip) need every workgroup of their grid resident at once: their
+// workgroups wait on words other workgroups publish.  Two such grids running
+// together on one device (two sessions or batchers stepping from different
+// threads, each on its own stream) can each hold part of the CUs, and their
+// bounded waits then time out.  Every session and batcher launch therefore
+// goes through this process-wide gate: a launch on a stream other than the
+// last one that used the device is first ordered after everything that
+// stream had enqueued (an event recorded there, waited on here), so the
+// device runs the steps one at a time.  Launches on one stream are ordered
+// by the stream itself and pay nothing extra.
+struct CoopGate {
+    std::mutex mu;
+    hipStream_t last = nullptr;
+    hipEvent_t ev = nullptr;
+};
+static CoopGate g_gate[16];
+
+template <typename F>
+static int gated_launch(int device, hipStream_t st, F&& launch) {
+    CoopGate& g = g_gate[device & 15];
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.last && g.last != st) {
+        if (!g.ev) HIP_OR_FAIL(hipEventCreateWithFlags(&g.ev, hipEventDisableTiming));
+        HIP_OR_FAIL(hipEventRecord(g.ev, g.last));
+        HIP_OR_FAIL(hipStreamWaitEvent(st, g.ev, 0));
+    }
+    const int rc = launch();
+    g.last = st;
+    return rc;
+}
+// A stream about to be destroyed stops being the gate's reference point
+// (its work is complete: the caller synchronised it).
+static void gate_forget(int device, hipStream_t st) {
+    CoopGate& g = g_gate[device & 15];
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.last == st) g.last = nullptr;
 }
 
 // ------------------------------------------------------------------ weights
@@ -336,7 +378,6 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
                                            int llama_permuted, lkhip_engine** out) {
     if (!cfg || !out || (!tensors && n_tensors)) return fail(LKHIP_E_INVALID, "engine: null argument");
     *out = nullptr;
-    if (lkhip_device_count() == 0) return fail(LKHIP_E_HIP, "no HIP device visible — the hip backend needs an AMD GPU");
     auto e = std::make_unique<lkhip_engine>();
     e->cfg = *cfg;
     if (!cfg->num_attention_heads || !cfg->num_key_value_heads || !cfg->hidden_size || !cfg->num_hidden_layers ||
@@ -349,6 +390,16 @@ extern "C" int lkhip_engine_create_tensors(const lkhip_config* cfg, const lkhip_
         cfg->num_attention_heads / cfg->num_key_value_heads > 8)
         return fail(LKHIP_E_UNSUPPORTED, "GQA group %u/%u is not supported — query heads per kv head must be 1..8",
                     cfg->num_attention_heads, cfg->num_key_value_heads);
+    // Per-head q/k RMSNorm (Qwen3-style self_attn.q_norm / k_norm, applied
+    // before RoPE at src/model.rs:213-222) is not computed by these kernels:
+    // refuse rather than run the layer without it.
+    for (size_t i = 0; i < n_tensors; i++) {
+        const char* nm = tensors[i].name;
+        if (nm && (strstr(nm, "self_attn.q_norm") || strstr(nm, "self_attn.k_norm")))
+            return fail(LKHIP_E_UNSUPPORTED,
+                        "%s: per-head q/k RMSNorm is not supported by the hip backend — use -b cpu", nm);
+    }
+    if (lkhip_device_count() == 0) return fail(LKHIP_E_HIP, "no HIP device visible — the hip backend needs an AMD GPU");
     e->qd = cfg->num_attention_heads * e->hd;
     e->kvd = cfg->num_key_value_heads * e->hd;
     (void)hipGetDevice(&e->device);
@@ -494,7 +545,11 @@ struct lkhip_session {
         for (auto v : ev) (void)hipEventDestroy(v);
         if (h_state) (void)hipHostFree(h_state);
         if (h_logits) (void)hipHostFree(h_logits);
-        if (stream) (void)hipStreamDestroy(stream);
+        if (stream) {
+            (void)hipStreamSynchronize(stream);
+            gate_forget(e ? e->device : 0, stream);
+            (void)hipStreamDestroy(stream);
+        }
     }
 };
 
@@ -777,19 +832,26 @@ static int set_state(lkhip_session* s, uint32_t token, size_t pos, uint32_t n_fe
 // Runs one step: graph replay, or eager with events when profiling.
 static int run_step(lkhip_session* s) {
     if (!s->profiling) {
-        if (s->exec) {
-            HIP_OR_FAIL(hipGraphLaunch(s->exec, s->stream));
-        } else {
-            Rec rec(s);
-            hipError_t err = enqueue_step(s, rec);
-            if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
-        }
-        return LKHIP_OK;
+        return gated_launch(s->e->device, s->stream, [&]() -> int {
+            if (s->exec) {
+                HIP_OR_FAIL(hipGraphLaunch(s->exec, s->stream));
+            } else {
+                Rec rec(s);
+                hipError_t err = enqueue_step(s, rec);
+                if (err != hipSuccess)
+                    return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
+            }
+            return LKHIP_OK;
+        });
     }
     Rec rec(s);
-    HIP_OR_FAIL(hipEventRecord(s->ev[0], s->stream));
-    hipError_t err = enqueue_step(s, rec);
-    if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
+    int rc = gated_launch(s->e->device, s->stream, [&]() -> int {
+        HIP_OR_FAIL(hipEventRecord(s->ev[0], s->stream));
+        hipError_t err = enqueue_step(s, rec);
+        if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step launch failed: %s", hipGetErrorString(err));
+        return LKHIP_OK;
+    });
+    if (rc) return rc;
     HIP_OR_FAIL(hipEventSynchronize(s->ev[rec.idx]));
     for (int i = 0; i < rec.idx; i++) {
         float ms = 0.f;
@@ -831,11 +893,12 @@ static int sync_check(lkhip_session* s) {
     uint32_t flag = 0;
     HIP_OR_FAIL(hipMemcpy(&flag, s->err.p, 4, hipMemcpyDeviceToHost));
     if (!flag) return LKHIP_OK;
-    if (flag & 2) {
-        HIP_OR_FAIL(hipMemset(s->err.p, 0, 4));
+    HIP_OR_FAIL(hipMemset(s->err.p, 0, 4));
+    if (!(flag & 1)) {
         return fail(LKHIP_E_HIP, "the lm_head launch timed out collecting its workgroups' argmax keys (is every CU "
                                  "free?) — the token and state of that step are invalid; restart from a known position");
     }
+    // bit 0: a wait inside the one-kernel step timed out (bit 1 may be set too)
     s->use_fused = false;
     if (s->exec) {
         (void)hipGraphExecDestroy(s->exec);
@@ -850,8 +913,9 @@ static int sync_check(lkhip_session* s) {
         int rc = build_graph(s);
         if (rc) return rc;
     }
-    return fail(LKHIP_E_HIP, "the one-kernel decode step timed out waiting on another workgroup (is every CU "
-                             "free?) — this session now runs the per-stage kernels; repeat the call");
+    return fail(LKHIP_E_HIP, "the one-kernel decode step%s timed out waiting on another workgroup (is every CU "
+                             "free?) — this session now runs the per-stage kernels; repeat the call",
+                flag & 2 ? " and the lm_head launch" : "");
 }
 
 static int copy_logits(lkhip_session* s, float* out) {
@@ -1357,8 +1421,11 @@ struct lkhip_batch {
         for (auto g : greedy_graph)
             if (g) (void)hipGraphExecDestroy(g);
         drop_fused_graphs();
-        if (stream) (void)hipStreamSynchronize(stream);
-        if (stream) (void)hipStreamDestroy(stream);
+        if (stream) {
+            (void)hipStreamSynchronize(stream);
+            gate_forget(e ? e->device : 0, stream);
+            (void)hipStreamDestroy(stream);
+        }
     }
 };
 
@@ -1435,9 +1502,11 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, bool fuse
                                       b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
     };
     if (!graphs_on()) {
-        hipError_t err = body(b->stream);
-        if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode_step launch failed: %s", hipGetErrorString(err));
-        return LKHIP_OK;
+        return gated_launch(b->e->device, b->stream, [&]() -> int {
+            hipError_t err = body(b->stream);
+            if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode_step launch failed: %s", hipGetErrorString(err));
+            return LKHIP_OK;
+        });
     }
     if (cache.size() <= n) cache.resize(n + 1, nullptr);
     if (!cache[n]) {
@@ -1457,8 +1526,10 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, bool fuse
             return fail(LKHIP_E_HIP, "instantiating the batched decode step failed: %s", hipGetErrorString(e3));
         }
     }
-    HIP_OR_FAIL(hipGraphLaunch(cache[n], b->stream));
-    return LKHIP_OK;
+    return gated_launch(b->e->device, b->stream, [&]() -> int {
+        HIP_OR_FAIL(hipGraphLaunch(cache[n], b->stream));
+        return LKHIP_OK;
+    });
 }
 
 extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_seq, lkhip_batch** out) {
@@ -1800,13 +1871,41 @@ extern "C" int lkhip_embed_gather(const lkhip_weight* table, const uint32_t* ids
     return LKHIP_OK;
 }
 
+// Shape checks shared by both attention entry points.
+static int attn_decode_check(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
+                             size_t n_heads, size_t n_kv_heads, size_t head_dim, float* out, const char* who) {
+    if (!q || !k_cache || !v_cache || !ctx_len || !out) return fail(LKHIP_E_INVALID, "%s: null argument", who);
+    if (head_dim != 64) return fail(LKHIP_E_UNSUPPORTED, "%s: head_dim %zu — 64 only", who, head_dim);
+    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
+        return fail(LKHIP_E_UNSUPPORTED, "%s: GQA group %zu/%zu not supported (1..8)", who, n_heads, n_kv_heads);
+    return LKHIP_OK;
+}
+
+static int attn_decode_launch(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
+                              size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t max_seq, float* out, float* part,
+                              void* stream) {
+    LkAttnArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.part = part;
+    a.ctx_len = ctx_len;
+    a.n_seq = (uint32_t)n_seq;
+    a.n_heads = (uint32_t)n_heads;
+    a.n_kv = (uint32_t)n_kv_heads;
+    a.max_seq = (uint32_t)max_seq;
+    a.seq_stride = (uint64_t)n_kv_heads * max_seq * 64;
+    a.q_stride = n_heads * 64;
+    LAUNCH_OR_FAIL(lk_attn_launch(a, (hipStream_t)stream));
+    return LKHIP_OK;
+}
+
 extern "C" int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                  const uint32_t* ctx_len, size_t n_seq, size_t n_heads, size_t n_kv_heads,
                                  size_t head_dim, size_t max_seq, float* out, void* stream) {
-    if (!q || !k_cache || !v_cache || !ctx_len || !out) return fail(LKHIP_E_INVALID, "attn_decode: null argument");
-    if (head_dim != 64) return fail(LKHIP_E_UNSUPPORTED, "attn_decode: head_dim %zu — 64 only", head_dim);
-    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
-        return fail(LKHIP_E_UNSUPPORTED, "attn_decode: GQA group %zu/%zu not supported (1..8)", n_heads, n_kv_heads);
+    int rc = attn_decode_check(q, k_cache, v_cache, ctx_len, n_heads, n_kv_heads, head_dim, out, "attn_decode");
+    if (rc) return rc;
     if (n_seq == 0 || max_seq == 0) return LKHIP_OK;
     // Partial buffer for this call, cached per thread and grown on demand.
     // (Deliberately never freed at thread exit: the HIP runtime may already be
@@ -1825,27 +1924,22 @@ extern "C" int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const 
         }
         part_bytes = need;
     }
-    LkAttnArgs a{};
-    a.q = q;
-    a.k = k_cache;
-    a.v = v_cache;
-    a.out = out;
-    a.part = (float*)part;
-    a.ctx_len = ctx_len;
-    a.n_seq = (uint32_t)n_seq;
-    a.n_heads = (uint32_t)n_heads;
-    a.n_kv = (uint32_t)n_kv_heads;
-    a.max_seq = (uint32_t)max_seq;
-    a.seq_stride = (uint64_t)n_kv_heads * max_seq * 64;
-    a.q_stride = n_heads * 64;
-    LAUNCH_OR_FAIL(lk_attn_launch(a, (hipStream_t)stream));
-    return LKHIP_OK;
+    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, (float*)part,
+                              stream);
 }
 
 extern "C" int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream) {
     if ((!x || !out) && n_rows) return fail(LKHIP_E_INVALID, "argmax: null argument");
     LAUNCH_OR_FAIL(lk_argmax_rows_launch(x, (uint32_t)n_rows, (uint32_t)n, out, (hipStream_t)stream));
     return LKHIP_OK;
+}
+
+extern "C" int lkhip_context_window(size_t window, size_t sink) {
+    if (window == 0) return LKHIP_OK;
+    return fail(LKHIP_E_UNSUPPORTED,
+                "--context-window needs a GPU-windowed backend — -b hip keeps the whole KV cache resident (window %zu, "
+                "sink %zu refused); drop the flag or use -b metal, -b hybrid, or -b lowmem",
+                window, sink);
 }
 
 extern "C" int lkhip_gguf_config(const char* path, lkhip_config* cfg_out, size_t* n_tensors_out,

@@ -128,7 +128,7 @@ __global__ __launch_bounds__(HT) void lm_head_kernel(const LkHeadArgs a) {
         b = o > b ? o : b;
     }
     if (__any(timed_out)) {
-        if (lane == 0) __hip_atomic_store(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) (void)__hip_atomic_fetch_or(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps bit 0 (one-kernel step) if set
         return;
     }
     if (lane == 0) {

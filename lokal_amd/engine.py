@@ -23,11 +23,21 @@ from ._lib import Config, LokalHipError, Profile, Row, TensorDesc, check, lib
 from .config import ModelConfig
 
 
-def create(backend: str, cfg: ModelConfig, tensors, llama_permuted: bool = False) -> "Engine":
-    """engine::create by backend name (src/engine.rs:76-111); this build has one: "hip"."""
+def create(backend: str, cfg: ModelConfig, tensors, llama_permuted: bool = False,
+           win: tuple[int, int] | None = None) -> "Engine":
+    """engine::create by backend name (src/engine.rs:76-111); this build has one: "hip".
+    win = (context window, attention sink) as src/main.rs:159-162 builds it;
+    the hip backend refuses a window (lkhip_context_window)."""
     if backend != "hip":
         raise LokalHipError(-1, f'unknown backend "{backend}" — available: hip')
+    check_window(win)
     return Engine.from_tensors(cfg, tensors, llama_permuted)
+
+
+def check_window(win: tuple[int, int] | None) -> None:
+    """The hip arm's --context-window contract (src/engine.rs:84-87 for the CPU arm)."""
+    if win is not None:
+        check(lib().lkhip_context_window(max(int(win[0]), 1), int(win[1])))
 
 
 def _cfg_struct(cfg: ModelConfig) -> Config:
@@ -90,8 +100,10 @@ class Engine:
         return cls(h, cfg)
 
     @classmethod
-    def from_gguf(cls, path: str) -> "Engine":
-        """engine::create_metal_quant's counterpart: weights stay quantized."""
+    def from_gguf(cls, path: str, win: tuple[int, int] | None = None) -> "Engine":
+        """engine::create_metal_quant's counterpart (src/engine.rs:150-162):
+        weights stay quantized; a context window is refused as check_window does."""
+        check_window(win)
         h = C.c_void_p()
         check(lib().lkhip_engine_create_gguf(str(path).encode(), C.byref(h)))
         c = Config()

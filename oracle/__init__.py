@@ -34,6 +34,17 @@ class OracleConfig(C.Structure):
     ]
 
 
+def select(variant: str) -> None:
+    """Chooses the build this process loads, before its first use: "o2" (the
+    parity build every test checks against, the default) or "o3" (the same
+    source at -O3 -mavx2, bit-identical results, timed as the CPU baseline)."""
+    global _LIB_PATH
+    path = {"o2": _HERE / "liblokal_oracle.so", "o3": _HERE / "liblokal_oracle_o3.so"}[variant]
+    if _lib is not None and path != _LIB_PATH:
+        raise RuntimeError(f"oracle: {_LIB_PATH.name} is already loaded in this process")
+    _LIB_PATH = path
+
+
 def lib():
     global _lib
     if _lib is None:

@@ -81,3 +81,30 @@ def test_headline_config_bytes_per_token():
     weights = L * per_layer + V * h
     assert weights == 493_961_216
     assert weights * 34 // 32 == 524_833_792
+
+
+def test_context_window_refused_with_a_reason():
+    """The hip arm refuses --context-window as the CPU arm does (src/engine.rs:84-87)."""
+    from lokal_amd import LokalHipError, create
+    from lokal_amd.engine import check_window
+    L = _lib.lib()
+    assert L.lkhip_context_window(0, 0) == 0
+    assert L.lkhip_context_window(512, 4) == -2
+    msg = L.lkhip_last_error().decode()
+    assert "--context-window" in msg and "-b metal" in msg and "\n" not in msg
+    check_window(None)
+    with pytest.raises(LokalHipError, match="context-window"):
+        create("hip", CONFIGS["qwen2.5-0.5b"], [], win=(1024, 4))
+
+
+def test_per_head_qk_norm_refused_before_any_device_work():
+    """A Qwen3-style tensor set (self_attn.q_norm / k_norm, src/model.rs:213-222)
+    is refused by name, not run without the norm -- also with no GPU present."""
+    from lokal_amd import Engine, LokalHipError
+    cfg = ModelConfig(256, 512, 1, 4, 2, 300, 1e-6)
+    tensors = synth.synth_model(cfg, synth.Q8_0, 0)
+    qn = synth.Tensor("model.layers.0.self_attn.q_norm.weight", _lib.LKHIP_F32, (64,),
+                      np.ones(64, np.float32))
+    with pytest.raises(LokalHipError, match="q_norm.*per-head q/k RMSNorm") as ei:
+        Engine.from_tensors(cfg, tensors + [qn])
+    assert ei.value.code == -2

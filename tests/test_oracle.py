@@ -306,3 +306,41 @@ def test_f32_to_f16_round_to_nearest_even():
     want = xs.astype(np.float16).view(np.uint16)
     assert np.array_equal(got, want)
     assert oracle.f32_to_f16(float("nan")) & 0x7c00 == 0x7c00
+
+
+_O3_SCRIPT = r"""
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+import oracle
+from lokal_amd import synth
+from lokal_amd.config import ModelConfig
+oracle.select("o3")
+oracle.set_threads(4)
+cfg = ModelConfig(576, 1536, 2, 9, 3, 2048, 1e-5, 1e4)
+m = oracle.Model(cfg, synth.synth_model(cfg, synth.Q8_0, seed=3, qkv_bias=True))
+s = m.session(40)
+out = [s.prefill(np.arange(1, 31, dtype=np.uint32) * 61)]
+for i in range(5):
+    out.append(s.forward(int(oracle.argmax(out[-1])), 30 + i))
+np.save(sys.argv[2], np.stack(out))
+"""
+
+
+def test_o3_baseline_build_is_bit_identical(tmp_path):
+    """The -O3 -mavx2 build timed as bench.py's CPU baseline computes the same
+    bits as the -O2 parity build (vectorised lanes round as scalar ones; no
+    contraction): prefill + 5 greedy steps of a 2-layer model, logits compared
+    as raw bits."""
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parent.parent
+    out = tmp_path / "o3.npy"
+    subprocess.run([sys.executable, "-c", _O3_SCRIPT, str(root), str(out)], check=True, timeout=300)
+    cfg = ModelConfig(576, 1536, 2, 9, 3, 2048, 1e-5, 1e4)
+    m = oracle.Model(cfg, synth.synth_model(cfg, synth.Q8_0, seed=3, qkv_bias=True))
+    s = m.session(40)
+    ref = [s.prefill(np.arange(1, 31, dtype=np.uint32) * 61)]
+    for i in range(5):
+        ref.append(s.forward(int(oracle.argmax(ref[-1])), 30 + i))
+    got = np.load(out)
+    assert np.array_equal(np.stack(ref).view(np.uint32), got.view(np.uint32))
