@@ -269,6 +269,18 @@ int lkhip_embed_gather(const lkhip_weight* table, const uint32_t* ids, size_t n_
 int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
                       size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq, float* out,
                       void* stream);
+/* lkhip_attn_decode without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot call hipMalloc (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).  Same
+ * arguments, kernels and results as lkhip_attn_decode; the flash-decoding
+ * partials go to a fixed 8 MiB device buffer (2^21 floats) that each device
+ * holds for the life of the process.  Calls needing more partial floats than
+ * that (n_seq * n_heads * ceil(max_seq / 256) * 66) fail with LKHIP_E_INVALID.
+ * All calls on one device share the buffer: calls that overlap on a device
+ * (concurrent streams or threads) race. */
+int lkhip_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                              const uint32_t* ctx_len, size_t n_seq, size_t n_heads, size_t n_kv_heads,
+                              size_t head_dim, size_t max_seq, float* out, void* stream);
 /* Greedy argmax (src/sampler.rs:67-75, first max wins) of n_rows rows of n. */
 int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream);
 

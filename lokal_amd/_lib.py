@@ -119,6 +119,8 @@ SIGNATURES = {
     "lkhip_embed_gather": (C.c_int, [_P, _P, C.c_size_t, _P, _P]),
     "lkhip_attn_decode": (C.c_int, [_P, _P, _P, _P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
                                     _P, _P]),
+    "lkhip_attn_decode_noalloc": (C.c_int, [_P, _P, _P, _P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
+                                            C.c_size_t, _P, _P]),
     "lkhip_argmax": (C.c_int, [_P, C.c_size_t, C.c_size_t, _P, _P]),
 }
 

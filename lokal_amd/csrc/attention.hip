@@ -20,6 +20,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #define LK_HD 64
 #ifndef LK_ACHUNK
@@ -30,6 +31,32 @@
 
 uint32_t lk_attn_chunk(uint32_t) { return LK_ACHUNK; }
 
+// Fixed partial buffer of lkhip_attn_decode_noalloc, for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops).  Each
+// device holds its own copy for the life of the process.  In host code the
+// array's name is only a stand-in: its device address comes from
+// hipGetSymbolAddress, once per device (lk_attn_scratch below), and only that
+// address is ever passed to a kernel.  Every call on a device shares it, so
+// calls that overlap on one device race.
+static __device__ __align__(256) float scratch[LK_ATTN_SCRATCH_FLOATS];
+
+hipError_t lk_attn_scratch(float** out) {
+    static std::mutex mu;
+    static float* addr[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = (float*)p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
 
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq) {
     const size_t nch = (max_seq + LK_ACHUNK - 1) / LK_ACHUNK;

@@ -1928,6 +1928,26 @@ extern "C" int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const 
                               stream);
 }
 
+extern "C" int lkhip_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                         const uint32_t* ctx_len, size_t n_seq, size_t n_heads, size_t n_kv_heads,
+                                         size_t head_dim, size_t max_seq, float* out, void* stream) {
+    int rc = attn_decode_check(q, k_cache, v_cache, ctx_len, n_heads, n_kv_heads, head_dim, out,
+                               "attn_decode_noalloc");
+    if (rc) return rc;
+    if (n_seq == 0 || max_seq == 0) return LKHIP_OK;
+    if (n_seq > 0xFFFFFFFFu || max_seq > 0x7FFFFFFFu)
+        return fail(LKHIP_E_INVALID, "attn_decode_noalloc: n_seq or max_seq out of range");
+    const size_t need = lk_attn_part_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq);
+    if (need > LK_ATTN_SCRATCH_FLOATS)
+        return fail(LKHIP_E_INVALID,
+                    "attn_decode_noalloc: %zu sequences x %zu heads x %zu positions need %zu partial floats, more "
+                    "than its fixed %u-float (8 MiB) device buffer — use lkhip_attn_decode",
+                    n_seq, n_heads, max_seq, need, LK_ATTN_SCRATCH_FLOATS);
+    float* part = nullptr;
+    HIP_OR_FAIL(lk_attn_scratch(&part));
+    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, part, stream);
+}
+
 extern "C" int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream) {
     if ((!x || !out) && n_rows) return fail(LKHIP_E_INVALID, "argmax: null argument");
     LAUNCH_OR_FAIL(lk_argmax_rows_launch(x, (uint32_t)n_rows, (uint32_t)n, out, (hipStream_t)stream));

@@ -200,6 +200,11 @@ struct LkAttnArgs {
 uint32_t lk_attn_chunk(uint32_t max_seq);
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);
 hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st);
+// The fixed partial buffer of the no-allocation attention entry point:
+// LK_ATTN_SCRATCH_FLOATS floats (8 MiB) per device; lk_attn_scratch gives
+// the current device's address (looked up once per device).
+#define LK_ATTN_SCRATCH_FLOATS (2u << 20)
+hipError_t lk_attn_scratch(float** out);
 
 // Multi-row dequant-fused GEMM (gemm.hip): Y[b][n] = sum_k X[b][k] W[n][k]
 // for b < n_rows, the B-row form of the matvec (Linear::forward over a batch

@@ -138,6 +138,13 @@ def attn_decode(q: DeviceArray, k: DeviceArray, v: DeviceArray, ctx_len: DeviceA
                                   out.ptr, stream))
 
 
+def attn_decode_noalloc(q: DeviceArray, k: DeviceArray, v: DeviceArray, ctx_len: DeviceArray, n_seq: int,
+                        n_heads: int, n_kv_heads: int, head_dim: int, max_seq: int, out: DeviceArray,
+                        stream=None) -> None:
+    check(lib().lkhip_attn_decode_noalloc(q.ptr, k.ptr, v.ptr, ctx_len.ptr, n_seq, n_heads, n_kv_heads, head_dim,
+                                          max_seq, out.ptr, stream))
+
+
 def argmax(x: DeviceArray, n_rows: int, n: int, out: DeviceArray, stream=None) -> None:
     check(lib().lkhip_argmax(x.ptr, n_rows, n, out.ptr, stream))
 
