@@ -174,13 +174,17 @@ int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int whic
 int lkhip_session_set_profiling(lkhip_session* s, int on);
 int lkhip_session_profile(lkhip_session* s, lkhip_profile* out, int reset);
 /* Stage timeline of the one-kernel decode step (the phase table of
- * LOKAL_GPU_TIMING, src/gpu/metal.rs:3994-4270): block >= 0 records, for that
- * workgroup, a 100 MHz timestamp at the start, after the embedding, after each
- * of the 6 stages of every layer, after the final norm, after lm_head and at
- * the end (2 + 6*layers + 3 entries); block < 0 stops recording.
- * lkhip_session_trace copies the last step's timestamps. */
+ * LOKAL_GPU_TIMING, src/gpu/metal.rs:3994-4270): block >= 0 starts recording,
+ * for EVERY workgroup, a 100 MHz timestamp at the start, after the embedding,
+ * after each of the 6 stages of every layer and at the end, followed by 24
+ * sub-step marks of layer 1 (2 + 6*layers + 1 + 24 entries per workgroup);
+ * `block` names the workgroup stage_times-style summaries report; block < 0
+ * stops recording.  lkhip_session_trace copies the last step's timestamps,
+ * [workgroup][entries]; lkhip_session_trace_len gives their number (0 when
+ * tracing is off). */
 int lkhip_session_set_trace(lkhip_session* s, int block);
 int lkhip_session_trace(lkhip_session* s, uint64_t* ticks, size_t n);
+size_t lkhip_session_trace_len(const lkhip_session* s);
 
 /* Engine::batcher (src/engine.rs:23-26): n_slots KV slots of max_seq positions,
  * pool laid out per layer as [slot][kv_head][max_seq][head_dim] f16. */

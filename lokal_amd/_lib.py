@@ -85,6 +85,7 @@ SIGNATURES = {
     "lkhip_session_set_profiling": (C.c_int, [_P, C.c_int]),
     "lkhip_session_profile": (C.c_int, [_P, C.POINTER(Profile), C.c_int]),
     "lkhip_session_set_trace": (C.c_int, [_P, C.c_int]),
+    "lkhip_session_trace_len": (C.c_size_t, [_P]),
     "lkhip_session_trace": (C.c_int, [_P, C.POINTER(C.c_uint64), C.c_size_t]),
     "lkhip_batch_create": (C.c_int, [_P, C.c_size_t, C.c_size_t, C.POINTER(_P)]),
     "lkhip_batch_destroy": (None, [_P]),

@@ -1026,16 +1026,23 @@ extern "C" int lkhip_session_set_trace(lkhip_session* s, int block) {
     if (!s->use_fused) return fail(LKHIP_E_UNSUPPORTED, "stage tracing needs the one-kernel decode step");
     if (block >= (int)s->e->fused_blocks) return fail(LKHIP_E_INVALID, "trace block %d out of range", block);
     if (block >= 0 && !s->trace.p) {
-        int rc = dev_alloc(s->trace, lk_fused_trace_len(s->e->cfg.num_hidden_layers) * 8);
+        int rc = dev_alloc(s->trace, (size_t)s->e->fused_blocks * lk_fused_trace_len(s->e->cfg.num_hidden_layers) * 8);
         if (rc) return rc;
     }
     s->trace_block = block < 0 ? -1 : block;
     return rebuild_graph(s);
 }
 
+static size_t trace_len(const lkhip_session* s) {
+    if (s->trace_block < 0) return 0;
+    return (size_t)s->e->fused_blocks * lk_fused_trace_len(s->e->cfg.num_hidden_layers);
+}
+
+extern "C" size_t lkhip_session_trace_len(const lkhip_session* s) { return s ? trace_len(s) : 0; }
+
 extern "C" int lkhip_session_trace(lkhip_session* s, uint64_t* ticks, size_t n) {
     if (!s || !ticks) return fail(LKHIP_E_INVALID, "null argument");
-    const size_t len = lk_fused_trace_len(s->e->cfg.num_hidden_layers);
+    const size_t len = trace_len(s);
     if (s->trace_block < 0) return fail(LKHIP_E_INVALID, "stage tracing is off");
     if (n < len) return fail(LKHIP_E_INVALID, "trace needs %zu entries", len);
     HIP_OR_FAIL(hipStreamSynchronize(s->stream));

@@ -34,9 +34,10 @@ struct LkFusedArgs {
     uint64_t* ab;   // [2][qd]       attention output
     uint64_t* xpb;  // [2][h]        x after the attention residual
     uint64_t* ib;   // [2][I]        SwiGLU output
-    // optional stage timestamps (s_memrealtime, 100 MHz) of one block:
-    // [0] start, [1] after the embedding, [2 + 6L + s] after stage s of layer
-    // L, then at the end of the block
+    // optional stage timestamps (s_memrealtime, 100 MHz), one row of
+    // lk_fused_trace_len entries per workgroup: [0] start, [1] after the
+    // embedding, [2 + 6L + s] after stage s of layer L, then at the end of
+    // the block
     uint64_t* trace;
     uint32_t trace_block;
     // Batcher rows (fused_rows.hip only): meta = u32 [ids | pos | slots | ...],

@@ -46,8 +46,8 @@
 // TinyLlama Q4_K: 1 + 1 (1493; 3 + 2: 1226).
 #define LKF_KB (WT == LK_Q8_0 ? 2 : 1)
 #define LKF_KA (WT == LK_Q8_0 ? 2 : 1)
-// Stage timestamps of the traced block (thread 0), kept in LDS and copied
-// out at the end so that tracing adds no global-memory traffic mid-stage;
+// Stage timestamps of every block (thread 0), kept in LDS and copied out at
+// the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
 #define LKF_MARK(k)                                                 \
     do {                                                            \
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         else if (hh < nh + nkv) { kind = 1; head = hh - nh; }
         else { kind = 2; head = hh - nh - nkv; }
     }
-    const bool tracing = a.trace && blockIdx.x == a.trace_block;
+    const bool tracing = a.trace != nullptr;  // every workgroup records its own row
     if (tracing && threadIdx.x == 0)
         for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) ltr[k] = 0;
     Row<WT, NCHH> q1, q2;  // prefetched one stage ahead (layer L's rows during layer L-1's down)
@@ -557,7 +557,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     LKF_MARK(2 + 6 * nL);
     if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch[0] = base + 1;
     if (tracing && threadIdx.x == 0)
-        for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) a.trace[k] = ltr[k];
+        for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) a.trace[(size_t)blockIdx.x * lk_fused_trace_len(nL) + k] = ltr[k];
 }
 
 }  // namespace lkf

@@ -193,14 +193,21 @@ class Session:
         """Record the stage timeline of workgroup `block` (< 0: stop)."""
         check(lib().lkhip_session_set_trace(self._h, int(block)))
 
-    def stage_times_us(self) -> dict:
-        """Stage durations (us) of the last one-kernel step, for the traced block
+    def trace_ticks(self) -> np.ndarray:
+        """Timestamps (100 MHz) of the last one-kernel step, [workgroup][2 + 6L + 1 + 24]:
+        start, after the embedding, after each of the 6 stages of every layer, end,
+        then 24 sub-step marks of layer 1."""
+        n = int(lib().lkhip_session_trace_len(self._h))
+        t = np.zeros(max(n, 1), dtype=np.uint64)
+        check(lib().lkhip_session_trace(self._h, t.ctypes.data_as(C.POINTER(C.c_uint64)), n))
+        L = self.engine.cfg.num_hidden_layers
+        return t.reshape(-1, 2 + 6 * L + 1 + 24)
+
+    def stage_times_us(self, block: int = 0) -> dict:
+        """Stage durations (us) of the last one-kernel step, for one workgroup
         (the final norm + lm_head + argmax is a separate launch, not traced)."""
         L = self.engine.cfg.num_hidden_layers
-        n = 2 + 6 * L + 1 + 24  # stage marks, end of block, then sub-steps of layer 1
-        t = np.zeros(n, dtype=np.uint64)
-        check(lib().lkhip_session_trace(self._h, t.ctypes.data_as(C.POINTER(C.c_uint64)), n))
-        t = t[:n - 24]
+        t = self.trace_ticks()[block][:2 + 6 * L + 1]
         us = np.diff(t.astype(np.float64)) / 100.0  # 100 MHz counter
         names = ["qkv", "attn", "merge", "o_proj", "gate_up", "down"]
         per = us[1:1 + 6 * L].reshape(L, 6)
