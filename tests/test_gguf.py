@@ -2,13 +2,17 @@
 header walk, metadata, alignment, dim reversal, names, bounds and refusals on
 the CPU (src/gguf/container.rs:162-261, src/gguf/arch.rs:164-270 and the
 reference's own container tests, whose tiny-file fixture is rebuilt here);
-on the GPU, an engine from a written file runs exactly like one from the
-same tensors."""
+on the GPU, an engine from a written file against the oracle loading the same
+file bytes the way load_f32 does (src/gguf/dequant.rs:538-557), including
+the llama q/k permutation (src/gguf/arch.rs:274-286), and against an engine
+from the same tensors."""
 import struct
 
 import numpy as np
 import pytest
 
+import oracle
+from oracle.gguf import read_gguf
 from tests.gguf_writer import write_gguf
 from lokal_amd import Engine, LokalHipError, gguf_config, synth
 from lokal_amd.config import ModelConfig
@@ -149,3 +153,73 @@ def test_engine_from_gguf_matches_engine_from_tensors(tmp_path, arch, wtype, bia
     sb.close()
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("arch,wtype", [("qwen2", synth.Q8_0), ("llama", synth.Q4_K), ("llama", synth.F16)])
+def test_oracle_reads_the_file_as_load_f32_does(tmp_path, arch, wtype):
+    """The oracle's reader of the file bytes (oracle/gguf.py) returns the
+    written config and tensors under HF names; a llama file's q/k rows come
+    back in the converter's order (not the HF order written), and the oracle
+    model built from the file with the permutation undone computes the same
+    bits as the model built from the HF tensors."""
+    cfg = TINY if wtype != synth.Q4_K else TINY.with_(hidden_size=512, intermediate_size=1024,
+                                                      num_attention_heads=8)
+    tensors = synth.synth_model(cfg, wtype, 11, tied=(arch == "qwen2"), qkv_bias=(arch == "qwen2"))
+    p = tmp_path / "o.gguf"
+    write_gguf(p, cfg, tensors, arch=arch)
+    fcfg, ft, permuted = read_gguf(p)
+    assert permuted == (arch == "llama")
+    for f in ("hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+              "num_key_value_heads", "vocab_size", "max_position_embeddings"):
+        assert getattr(fcfg, f) == getattr(cfg, f), f
+    assert np.float32(fcfg.rms_norm_eps) == np.float32(cfg.rms_norm_eps)
+    assert np.float32(fcfg.rope_theta) == np.float32(cfg.rope_theta)
+    want = {t.name: t for t in tensors}
+    assert sorted(t.name for t in ft) == sorted(want)
+    for t in ft:
+        w = want[t.name]
+        assert t.ggml_type == w.ggml_type and tuple(t.dims) == tuple(w.dims), t.name
+        same = np.array_equal(t.data, np.asarray(w.data).view(np.uint8).reshape(-1))
+        qk = t.name.endswith(("q_proj.weight", "k_proj.weight"))
+        assert same != (qk and arch == "llama"), t.name
+    a, b = oracle.Model(fcfg, ft, llama_permuted=permuted), oracle.Model(cfg, tensors)
+    sa, sb = a.session(16), b.session(16)
+    for pos, tok in enumerate((3, 77, 150, 299)):
+        assert np.array_equal(sa.forward(tok, pos), sb.forward(tok, pos))
+    a.close()
+    b.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arch,wtype,bias", [("qwen2", synth.Q8_0, True), ("llama", synth.Q4_K, False),
+                                             ("llama", synth.F16, False), ("llama", synth.Q8_0, False)])
+def test_engine_from_gguf_matches_oracle_from_the_same_bytes(tmp_path, arch, wtype, bias):
+    """GGUF engine (HIP reader, upload-time unpermute) against the oracle built
+    from the same file's bytes with load_f32's rule (llama q/k unpermuted):
+    logits within 1e-3 over 24 positions (f32 KV caches on both sides) and
+    identical greedy ids for 24 steps."""
+    cfg = TINY if wtype != synth.Q4_K else TINY.with_(hidden_size=512, intermediate_size=1024,
+                                                      num_attention_heads=8)
+    tensors = synth.synth_model(cfg, wtype, 13, tied=(arch == "qwen2"), qkv_bias=bias)
+    p = tmp_path / "x.gguf"
+    write_gguf(p, cfg, tensors, arch=arch)
+    del tensors
+    fcfg, ft, permuted = read_gguf(p)
+    eng = Engine.from_gguf(str(p))
+    om = oracle.Model(fcfg, ft, llama_permuted=permuted)
+    s, o = eng.session(64, kv_dtype="f32"), om.session(64)
+    toks = np.random.default_rng(14).integers(0, cfg.vocab_size, 24)
+    for pos, t in enumerate(toks):
+        got, want = s.forward(int(t), pos), o.forward(int(t), pos)
+        err = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+        assert err < 1e-3, (arch, pos, err)
+    first = int(oracle.argmax(want))
+    ids = list(s.decode_greedy(first, len(toks), 24))
+    cur, ref = first, []
+    for i in range(24):
+        cur = int(oracle.argmax(o.forward(cur, len(toks) + i)))
+        ref.append(cur)
+    assert ids == ref
+    s.close()
+    eng.close()
+    om.close()

@@ -244,3 +244,13 @@ def test_greedy_64_steps_identical_with_f16_kv(name):
     agree within TOL_F16_KV and whose top-2 gap lies inside that band: with
     f16 K/V, a one-ulp rounding flip can reorder such a near-tie."""
     _greedy_identity(name, "f16", allow_near_tie=True)
+
+
+@pytest.mark.parametrize("name,prompt_len", [("qwen2.5-0.5b-q8_0", 512), ("smollm2-135m", 512),
+                                             ("tinyllama-1.1b-q4_k", 256)])
+def test_greedy_64_steps_at_the_configs_prompt_lengths_f32_kv(name, prompt_len):
+    """BASELINE configs 3 and 1 (512-token prompt) and 4 (256-token prompt): the
+    prompt through Session::prefill, then 64 greedy steps on the one-kernel
+    step at positions 512..575 (256..319), ids identical to the CPU path's and
+    logits within 1e-3, f32 KV caches on both sides (src/generate.rs:80-118)."""
+    _greedy_identity(name, "f32", prompt_len=prompt_len, seed=4)
