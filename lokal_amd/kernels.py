@@ -149,6 +149,14 @@ def argmax(x: DeviceArray, n_rows: int, n: int, out: DeviceArray, stream=None) -
     check(lib().lkhip_argmax(x.ptr, n_rows, n, out.ptr, stream))
 
 
+def memset(d: DeviceArray, value: int) -> None:
+    check(lib().lkhip_memset(d.ptr, value, d.nbytes))
+
+
+def memcpy_dtod(dst: DeviceArray, src: DeviceArray) -> None:
+    check(lib().lkhip_memcpy_dtod(dst.ptr, src.ptr, min(dst.nbytes, src.nbytes)))
+
+
 def synchronize() -> None:
     check(lib().lkhip_synchronize())
 

@@ -18,6 +18,18 @@ Prints one JSON object per measurement:
           GB/s (each weight byte read once per launch) and fp32 TFLOP/s;
   prefill config 3's 512-token prompt through Session::prefill, chunked on
           the GEMM path and as the per-token loop (LKHIP_PREFILL=loop);
+  matvec  lkhip_q8_0_matvec (the per-stage dequant-fused matvec) alone at
+          the Qwen2.5-0.5B decode shapes 896->896 (q, o_proj), 896->128 (k,
+          v), 896->4864 (gate, up), 4864->896 (down), 896->151936 (lm_head):
+          a HIP graph of launches that cycle through enough copies of the
+          matrix (>= 512 MiB, so the 256 MB Infinity Cache cannot hold them)
+          that every launch streams from HBM; µs per launch, GB/s of the
+          Q8_0 bytes and % of 8 TB/s;
+  mix     a short run of every decode-step kernel family, for profiler
+          counter passes (rocprofv3 --pmc): 8 greedy tokens of config 3
+          (fused_step_kernel, lm_head_kernel), one config-5 step of 24
+          layers at 4096 positions (attn_mfma_kernel, attn_merge_kernel), 8
+          batched greedy steps of 4 rows (fused_rows_kernel);
   batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
           with a 512-token prompt, then 64 greedy steps of all B rows on the
           device: aggregate tok/s and weight GB/s (one weight read per step).
@@ -62,6 +74,19 @@ def _hip():
               "hipGraphExecDestroy", "hipGraphDestroy"):
         getattr(h, f).restype = ctypes.c_int
     return h
+
+
+def _timed_graph_seq(fns, rounds: int, stream: K.Stream) -> float:
+    """Average ms per launch of the launches fns, captured `rounds` times in
+    order into one HIP graph."""
+    it = iter(range(len(fns) * rounds))
+    calls = [fns[i % len(fns)] for i in it]
+    state = {"i": 0}
+
+    def step():
+        calls[state["i"] % len(calls)]()
+        state["i"] += 1
+    return _timed_graph(step, len(calls), stream)
 
 
 def _timed_graph(fn, reps: int, stream: K.Stream) -> float:
@@ -273,9 +298,76 @@ def batch() -> list[dict]:
     return out
 
 
+def matvec() -> list[dict]:
+    st = K.Stream()
+    out = []
+    rng = np.random.default_rng(3)
+    for name, rows, cols in (("q_proj/o_proj", 896, 896), ("k_proj/v_proj", 128, 896), ("gate/up", 4864, 896),
+                             ("down", 896, 4864), ("lm_head", 151936, 896)):
+        data = synth.gen_weight(synth.Q8_0, 5, "model.layers.0.mlp.up_proj.weight", rows, cols).data
+        nbytes = rows * cols * 34 // 32
+        copies = int(min(512, max(2, -(-(512 << 20) // nbytes))))
+        ws = [K.Weight(synth.Q8_0, rows, cols, data) for _ in range(copies)]
+        x = K.DeviceArray.from_numpy(rng.standard_normal(cols).astype(np.float32))
+        y = K.DeviceArray(rows)
+        fns = [(lambda w=w: K.q8_0_matvec(w, x, y, stream=st.ptr)) for w in ws]
+        rounds = max(1, 256 // copies)
+        ms = _timed_graph_seq(fns, rounds, st)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"bench": "q8_0_matvec", "shape": f"{cols}->{rows}", "matrix": name, "bytes": nbytes,
+                    "copies": copies, "resident_bytes": copies * nbytes, "launches": copies * rounds,
+                    "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        for w in ws:
+            w.close()
+    return out
+
+
+def mix() -> list[dict]:
+    from .engine import BatchRow
+    cfg, tensors = synth.synth_named("qwen2.5-0.5b-q8_0", 0)
+    eng = Engine.from_tensors(cfg, tensors)
+    del tensors
+    rng = np.random.default_rng(21)
+    s = eng.session(600)
+    tok = int(np.argmax(s.prefill(rng.integers(0, cfg.vocab_size, 512).astype(np.uint32))))
+    s.decode_greedy(tok, 512, 8)
+    s.close()
+    bat = eng.batcher(4, 600)
+    rows = []
+    for slot in range(4):
+        lg = bat.prefill(slot, rng.integers(0, cfg.vocab_size, 512).astype(np.uint32))
+        rows.append(BatchRow(int(np.argmax(lg)), 512, slot))
+    bat.decode_greedy(rows, 8)
+    bat.close()
+    eng.close()
+    st = K.Stream()
+    n_seq, nh, nkv, hd, ctx = 4, 14, 2, 64, 4096
+    kv = rng.standard_normal(n_seq * nkv * ctx * hd).astype(np.float16).view(np.uint16)
+    k, v = K.DeviceArray.from_numpy(kv), K.DeviceArray.from_numpy(kv[::-1].copy())
+    q = K.DeviceArray.from_numpy(rng.standard_normal((n_seq, nh * hd)).astype(np.float32))
+    cl = K.DeviceArray.from_numpy(np.full(n_seq, ctx, np.uint32))
+    o = K.DeviceArray((n_seq, nh * hd))
+    for _ in range(24):
+        K.attn_decode(q, k, v, cl, n_seq, nh, nkv, hd, ctx, o, st.ptr)
+    st.synchronize()
+    k.free()
+    v.free()
+    st.close()
+    # a plain device copy of 256 MiB (read 256, write 256), the reference the
+    # FETCH_SIZE / WRITE_SIZE counters of a --pmc pass are scaled by
+    n = 256 << 20
+    src, dst = K.DeviceArray(n, np.uint8), K.DeviceArray(n, np.uint8)
+    K.memset(src, 1)
+    K.memcpy_dtod(dst, src)
+    K.synchronize()
+    src.free()
+    dst.free()
+    return [{"workload": "mix", "done": True}]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--only", default="decode,layers,attn,gemm,prefill,batch")
+    ap.add_argument("--only", default="decode,layers,attn,gemm,prefill,batch,matvec")
     args = ap.parse_args()
     want = set(args.only.split(","))
     if K.device_count() == 0:
@@ -290,7 +382,7 @@ def main() -> int:
     if "attn" in want:
         for r in attn():
             print(json.dumps(r), flush=True)
-    for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch)):
+    for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch), ("matvec", matvec), ("mix", mix)):
         if name in want:
             for r in fn():
                 print(json.dumps(r), flush=True)
