@@ -277,11 +277,14 @@ int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
  * reference: it is for callers that cannot call hipMalloc (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation).  Same
  * arguments, kernels and results as lkhip_attn_decode; the flash-decoding
- * partials go to a fixed 8 MiB device buffer (2^21 floats) that each device
- * holds for the life of the process.  Calls needing more partial floats than
- * that (n_seq * n_heads * ceil(max_seq / 256) * 66) fail with LKHIP_E_INVALID.
- * All calls on one device share the buffer: calls that overlap on a device
- * (concurrent streams or threads) race. */
+ * arrival counters and partials go to a fixed 8 MiB device buffer (2^21
+ * floats) that each device holds for the life of the process: 1024
+ * counters 256 bytes apart (n_seq * n_kv_heads <= 1024), then
+ * n_seq * n_heads * C * 66 partial floats, C = min(32, ceil(max_seq / 64)).
+ * Larger calls fail with LKHIP_E_INVALID before any device work.  The
+ * counters start at zero and every call leaves them zero.  All calls on one
+ * device share the buffer: calls that overlap on a device (concurrent
+ * streams or threads) race. */
 int lkhip_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                               const uint32_t* ctx_len, size_t n_seq, size_t n_heads, size_t n_kv_heads,
                               size_t head_dim, size_t max_seq, float* out, void* stream);

@@ -1,10 +1,12 @@
-// attention.hip -- GQA flash-decoding over the f16 KV cache (model::attention,
+// attention.hip -- GQA flash-decoding over the KV cache (model::attention,
 // src/model.rs:286-318, computed split-K over positions and merged).
 //
-// One block = one (sequence, kv head, 256-position chunk).  The G query heads
-// that share the kv head are staged in LDS, so every K and V byte of the chunk
-// is read from HBM exactly once for the whole group.  Each of the 4 waves owns
-// a 64-position tile:
+// One block = one (sequence, kv head, chunk of 64*A*T positions).  The G
+// query heads that share the kv head are staged in LDS (or registers), so
+// every K and V byte of the chunk is read from HBM exactly once for the whole
+// group.  Each of the block's A active waves (A = 8, 4, 2 or 1 of its 8)
+// takes the 64-position tiles w, w+A, ... of the chunk with an online softmax
+// across them:
 //   scores : lane = position, the K row (128 B) is converted once and dotted
 //            against all G query rows (LDS broadcast reads);
 //   softmax: per-tile max / exp / sum by wave reductions;
@@ -13,9 +15,19 @@
 //            share a dim slice are combined by DPP.
 // Loads are straight-line (positions past ctx re-read the last live row and
 // are masked), issued before the dependent arithmetic.
-// The 4 tiles merge in LDS into one (m, l, acc[64]) partial per query head;
-// attn_merge_kernel folds the partials of all chunks with the usual
-// max-rescaled sums.  fp32 throughout; scale 1/sqrt(64) = 0.125 is exact.
+// The waves merge in LDS into one (m, l, acc[64]) partial per query head,
+// written with coherent stores; the block then counts itself in on its
+// (sequence, kv head) counter, and the block that arrives last folds every
+// chunk's partials (max-rescaled sums) into the output and clears the
+// counter -- one launch per layer, no separate merge kernel.  The host picks
+// A and T per launch (attn_plan): at most 32 chunks per (sequence, kv head),
+// so the fold reads each head's partials in one round trip, and, where the
+// cache is short, smaller chunks (A < 8) so the grid still has >= 128 blocks.
+// Few large chunks beat many small ones: each chunk costs a partial write,
+// an atomic on its counter and a share of the fold, and those counters sit
+// 256 bytes apart so the atomics of different (sequence, kv head) do not
+// contend for one cache line.
+// fp32 throughout; scale 1/sqrt(64) = 0.125 is exact.
 #include "lkhip_common.h"
 
 #include <cstdlib>
@@ -24,12 +36,45 @@
 
 #define LK_HD 64
 #ifndef LK_ACHUNK
-#define LK_ACHUNK 256
+#define LK_ACHUNK 512
 #endif
-#define LK_AW (LK_ACHUNK / 64)  // waves per partial block: one 64-position tile each
-#define LK_MB 32  // chunks per merge wave and round
+#define LK_AW (LK_ACHUNK / 64)  // waves per block: one 64-position tile each per round
+#ifndef LK_MAXCH
+#define LK_MAXCH 32  // chunks per (sequence, kv head) at most: the fold's loads per lane
+#endif
+#ifndef LK_ATTN_MINBLOCKS
+#define LK_ATTN_MINBLOCKS 128  // grid size below which the plan shrinks the chunk
+#endif
 
-uint32_t lk_attn_chunk(uint32_t) { return LK_ACHUNK; }
+// Partial slots per (sequence, head): every plan's chunk holds >= 64 positions.
+static inline uint32_t attn_chunk_cap(uint32_t max_seq) {
+    const uint32_t t = (max_seq + 63) / 64;
+    return t < LK_MAXCH ? t : LK_MAXCH;
+}
+struct AttnPlan {
+    uint32_t waves, tiles, chunks;  // active waves per block, tiles per wave, chunks per (seq, kvh)
+};
+// The largest A in 4, 2, 1 whose grid has >= 512 blocks, else the one with
+// the most blocks (the larger A on a tie), with T the fewest tiles per wave
+// that keep the chunks per (seq, kvh) <= 64.
+static AttnPlan attn_plan(uint32_t n_seq, uint32_t n_kv, uint32_t max_seq) {
+    AttnPlan best{};
+    for (uint32_t A = LK_AW; A >= 1; A /= 2) {
+        AttnPlan p{};
+        const uint32_t per = 64 * A * LK_MAXCH;
+        p.waves = A;
+        p.tiles = (max_seq + per - 1) / per;
+        if (!p.tiles) p.tiles = 1;
+        p.chunks = (max_seq + 64 * A * p.tiles - 1) / (64 * A * p.tiles);
+        if (!best.waves || p.chunks > best.chunks) best = p;
+        if ((uint64_t)p.chunks * n_kv * n_seq >= LK_ATTN_MINBLOCKS) return p;
+    }
+    return best;
+}
+uint32_t lk_attn_chunk(uint32_t max_seq) {
+    const AttnPlan p = attn_plan(1, 1, max_seq);
+    return 64 * p.waves * p.tiles;
+}
 
 // Fixed partial buffer of lkhip_attn_decode_noalloc, for callers that cannot
 // allocate device memory (code under HIP graph capture, serving loops).  Each
@@ -37,7 +82,8 @@ uint32_t lk_attn_chunk(uint32_t) { return LK_ACHUNK; }
 // array's name is only a stand-in: its device address comes from
 // hipGetSymbolAddress, once per device (lk_attn_scratch below), and only that
 // address is ever passed to a kernel.  Every call on a device shares it, so
-// calls that overlap on one device race.
+// calls that overlap on one device race.  Its arrival counters start at zero
+// (static storage) and every launch leaves them zero again.
 static __device__ __align__(256) float scratch[LK_ATTN_SCRATCH_FLOATS];
 
 hipError_t lk_attn_scratch(float** out) {
@@ -59,8 +105,7 @@ hipError_t lk_attn_scratch(float** out) {
 }
 
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq) {
-    const size_t nch = (max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
-    return (size_t)n_seq * n_heads * nch * (2 + LK_HD);
+    return (size_t)n_seq * n_heads * attn_chunk_cap(max_seq) * (2 + LK_HD);
 }
 
 __device__ __forceinline__ uint32_t attn_ctx(const LkAttnArgs& a, uint32_t seq) {
@@ -85,13 +130,104 @@ __device__ __forceinline__ void load8(const float* p, float* o) {
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
+
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// After a block has written its chunk partials (coherent stores): wait until
+// they are acknowledged, count the block in, and if it is the last of the
+// nch chunks of (seq, kvh), fold all of them into the output.  The partial
+// stores are write-through and complete before the count (s_waitcnt
+// vmcnt(0) + the barrier), and the folding block reads them with coherent
+// loads after seeing the count, so it sees every chunk's words; no cache
+// writeback is needed.  Wave w folds heads w, w+4: lane k holds chunk k's
+// (m, l), and every lane its dim of all chunks' acc -- one round trip for
+// the lot (nch <= LK_MAXCH = 64).
+template <int G>
+__device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t nch) {
+    __shared__ uint32_t last;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t* cnt = a.cnt + ((size_t)seq * a.n_kv + kvh) * LK_ATTN_CNT_STRIDE;
+        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+#pragma unroll
+    for (int r = 0; r < (8 + LK_AW - 1) / LK_AW; r++) {
+        const uint32_t g = (uint32_t)w + LK_AW * r;
+        if (g >= (uint32_t)G) break;
+        const uint32_t h = kvh * G + g;
+        const float* ph = a.part + ((size_t)seq * a.n_heads + h) * a.cstride * (2 + LK_HD);
+        const bool live = (uint32_t)lane < nch;
+        const float* pk = ph + (size_t)(live ? lane : 0) * (2 + LK_HD);
+        const float mk = ld_coherent(pk), lk = ld_coherent(pk + 1);
+        float av[LK_MAXCH];
+#pragma unroll
+        for (int k = 0; k < LK_MAXCH; k++) {
+            const uint32_t c = (uint32_t)k < nch ? (uint32_t)k : 0u;  // in-range reload, weighted 0 below
+            av[k] = ld_coherent(ph + (size_t)c * (2 + LK_HD) + 2 + lane);
+        }
+        const float M = lk_wave_max(live ? mk : -INFINITY);  // finite: chunk 0 is live
+        const float sck = live ? expf(mk - M) : 0.f;          // chunk k's weight, held by lane k
+        const float L = lk_wave_sum(sck * lk);
+        float A = 0.f;
+#pragma unroll
+        for (int k = 0; k < LK_MAXCH; k++) {
+            const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sck), k));
+            A = fmaf(sk, av[k], A);
+        }
+        a.out[((size_t)seq * a.n_heads + h) * LK_HD + lane] = A / L;
+    }
+    if (tid == 0)
+        __hip_atomic_store(a.cnt + ((size_t)seq * a.n_kv + kvh) * LK_ATTN_CNT_STRIDE, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The 4 waves' (m, l, acc) of each head (red_m[w][g] etc.) -> the chunk's
+// partial per head, with coherent stores.
+template <int G, typename RM, typename RA>
+__device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t chunk,
+                                                    const RM& red_m, const RM& red_l, const RA& red_acc) {
+    float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * a.cstride + chunk) * (2 + LK_HD);
+    for (int t = threadIdx.x; t < G * LK_HD; t += LK_AW * 64) {
+        const int g = t / LK_HD, d = t % LK_HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < LK_AW; ww++) {
+            if (red_m[ww][g] != -INFINITY) {
+                const float sc = expf(red_m[ww][g] - M);
+                L = fmaf(sc, red_l[ww][g], L);
+                A = fmaf(sc, red_acc[ww][g][d], A);
+            }
+        }
+        float* ph = part + (size_t)g * a.cstride * (2 + LK_HD);
+        if (d == 0) {
+            st_coherent(ph, M);
+            st_coherent(ph + 1, L);
+        }
+        st_coherent(ph + 2 + d, A);
+    }
+}
+
 template <int G, typename KV>
 __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnArgs a) {
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t ctx = attn_ctx(a, seq);
-    const uint32_t c0 = chunk * LK_ACHUNK;
+    const uint32_t A = a.waves, T = a.tiles, CH = 64 * A * T;
+    const uint32_t c0 = chunk * CH;
     if (c0 >= ctx) return;  // uniform over the block
-    const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
+    const uint32_t nch = (ctx + CH - 1) / CH;
     const uint32_t slot = a.slots ? a.slots[seq] : seq;
     const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
     const KV* __restrict__ K = (const KV*)a.k + kv_base;
@@ -104,18 +240,7 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t p0 = c0 + (uint32_t)w * 64;
-    const bool tile_live = p0 < ctx;  // wave-uniform
     const uint32_t plast = ctx - 1;
-    // Straight-line loads: positions past ctx re-read the last live row (in
-    // bounds) and are masked below.  K: lane = position, its whole 64-dim row.
-    const uint32_t p = p0 + (uint32_t)lane;
-    const KV* krow = K + (size_t)(p < ctx ? p : plast) * LK_HD;
-    float kf[LK_HD];
-    if (tile_live) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) load8(krow + 8 * i, kf + 8 * i);
-    }
     const float* qsrc = a.q + (size_t)seq * a.q_stride + (size_t)kvh * G * LK_HD;
     for (int i = tid; i < G * LK_HD; i += LK_AW * 64) qs[i / LK_HD][i % LK_HD] = qsrc[i];
     __syncthreads();
@@ -130,7 +255,16 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
     }
-    if (tile_live) {
+    for (uint32_t t = 0; t < T && (uint32_t)w < A; t++) {
+        const uint32_t p0 = c0 + ((uint32_t)w + A * t) * 64;
+        if (p0 >= ctx) break;  // wave-uniform
+        // Straight-line loads: positions past ctx re-read the last live row (in
+        // bounds) and are masked below.  K: lane = position, its whole 64-dim row.
+        const uint32_t p = p0 + (uint32_t)lane;
+        const KV* krow = K + (size_t)(p < ctx ? p : plast) * LK_HD;
+        float kf[LK_HD];
+#pragma unroll
+        for (int i = 0; i < 8; i++) load8(krow + 8 * i, kf + 8 * i);
         // V for the P.V pass, issued before the scores so it is in flight meanwhile
         float vf[8][8];
 #pragma unroll
@@ -148,20 +282,25 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 const float4 qv = *(const float4*)&qs[g][4 * i];
-                float t = s[g];
-                t = fmaf(kf[4 * i], qv.x, t);
-                t = fmaf(kf[4 * i + 1], qv.y, t);
-                t = fmaf(kf[4 * i + 2], qv.z, t);
-                t = fmaf(kf[4 * i + 3], qv.w, t);
-                s[g] = t;
+                float u = s[g];
+                u = fmaf(kf[4 * i], qv.x, u);
+                u = fmaf(kf[4 * i + 1], qv.y, u);
+                u = fmaf(kf[4 * i + 2], qv.z, u);
+                u = fmaf(kf[4 * i + 3], qv.w, u);
+                s[g] = u;
             }
         }
+        // online softmax across this wave's tiles
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float sg = valid ? s[g] * 0.125f : -INFINITY;
-            m[g] = lk_wave_max(sg);
-            const float pg = valid ? expf(sg - m[g]) : 0.f;
-            l[g] = lk_wave_sum(pg);
+            const float mn = fmaxf(m[g], lk_wave_max(sg));  // finite: the tile holds a live position
+            const float sc = expf(m[g] - mn);                // 0 on the wave's first tile
+            const float pg = valid ? expf(sg - mn) : 0.f;
+            l[g] = fmaf(l[g], sc, lk_wave_sum(pg));
+            m[g] = mn;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] *= sc;
             ps[w][g][(lane & 7) * 8 + (lane >> 3)] = pg;  // position lane -> [group][jj]
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's P is in LDS
@@ -176,23 +315,25 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
                 for (int e = 0; e < 8; e++) acc[g][e] = fmaf(pw, vf[jj][e], acc[g][e]);
             }
         }
-        // sum the 8 position groups of each dims chunk (8 adjacent lanes) by
-        // DPP: quad pairs, quad halves, row_ror 4 -> lanes 4..7 of each 8 hold it
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float v = acc[g][e];
-                v += lk_dpp<0xB1, 0xF>(v, 0.f);
-                v += lk_dpp<0x4E, 0xF>(v, 0.f);
-                v += lk_dpp<0x124, 0xF>(v, 0.f);
-                acc[g][e] = v;
-            }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // the P reads are done before the next tile rewrites ps
+        __builtin_amdgcn_wave_barrier();
     }
+    // sum the 8 position groups of each dims chunk (8 adjacent lanes) by
+    // DPP: quad pairs, quad halves, row_ror 4 -> lanes 4..7 of each 8 hold it
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = acc[g][e];
+            v += lk_dpp<0xB1, 0xF>(v, 0.f);
+            v += lk_dpp<0x4E, 0xF>(v, 0.f);
+            v += lk_dpp<0x124, 0xF>(v, 0.f);
+            acc[g][e] = v;
+        }
     if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            red_m[w][g] = m[g];
+            red_m[w][g] = m[g];  // -inf for a wave with no live tile
             red_l[w][g] = l[g];
         }
     }
@@ -203,35 +344,14 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
             for (int e = 0; e < 8; e++) red_acc[w][g][dq + e] = acc[g][e];
     }
     __syncthreads();
-
-    // ---- merge the 4 tiles into one partial per query head
-    float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * max_chunks + chunk) * (2 + LK_HD);
-    for (int t = tid; t < G * LK_HD; t += LK_AW * 64) {
-        const int g = t / LK_HD, d = t % LK_HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < LK_AW; ww++) {
-            if (red_m[ww][g] != -INFINITY) {
-                const float sc = expf(red_m[ww][g] - M);
-                L = fmaf(sc, red_l[ww][g], L);
-                A = fmaf(sc, red_acc[ww][g][d], A);
-            }
-        }
-        float* ph = part + (size_t)g * max_chunks * (2 + LK_HD);
-        if (d == 0) {
-            ph[0] = M;
-            ph[1] = L;
-        }
-        ph[2 + d] = A;
-    }
+    write_chunk_partial<G>(a, seq, kvh, chunk, red_m, red_l, red_acc);
+    count_in_and_fold<G>(a, seq, kvh, nch);
 }
 
 // The f16-cache partial on the matrix cores.  Same block/tile split as
-// attn_partial_kernel (a 256-position chunk per block, a 64-position tile per
-// wave), with both products on v_mfma_f32_16x16x16f16:
+// attn_partial_kernel (a chunk of 256*T positions per block, 64-position
+// tiles w, w+4, ... per wave), with both products of a tile on
+// v_mfma_f32_16x16x16f16:
 //   scores : S[pos][head] = K . q, 16 positions x 16 heads (G used) per MFMA,
 //            K rows exact in f16, q split into f16 hi + lo (22 significant
 //            bits), f32 accumulation.  MFMA row m of sub-tile t is position
@@ -239,7 +359,8 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 //            lane l holds that row of K for m = l & 15, dims 16*(l >> 4) ..
 //            +15 -- the same dims for q -- so a wave's K load is 16 whole
 //            128-byte rows;
-//   softmax: per head (lane & 15) over the wave's 64 positions;
+//   softmax: per head (lane & 15) over the tile's 64 positions, folded into
+//            the wave's running (max, sum, O) across its tiles;
 //   P.V    : O[head][dim] = P . V with P straight from the score registers
 //            (lane l holds P[head l & 15][positions 4*(l >> 4) .. +3], exactly
 //            the A-operand layout), split hi + lo like q, and V read back from
@@ -265,9 +386,10 @@ template <int G>
 __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs a) {
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const uint32_t ctx = attn_ctx(a, seq);
-    const uint32_t c0 = chunk * LK_ACHUNK;
+    const uint32_t A = a.waves, T = a.tiles, CH = 64 * A * T;
+    const uint32_t c0 = chunk * CH;
     if (c0 >= ctx) return;  // uniform over the block
-    const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
+    const uint32_t nch = (ctx + CH - 1) / CH;
     const uint32_t slot = a.slots ? a.slots[seq] : seq;
     const size_t kv_base = (size_t)slot * a.seq_stride + (size_t)kvh * a.max_seq * LK_HD;
     const uint16_t* __restrict__ K = (const uint16_t*)a.k + kv_base;
@@ -282,28 +404,8 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t j = (uint32_t)lane >> 4, c16 = (uint32_t)lane & 15;
-    const uint32_t p0 = c0 + (uint32_t)w * 64;
-    const bool tile_live = p0 < ctx;  // wave-uniform
     const uint32_t plast = ctx - 1;
 
-    // K: sub-tile t rows p0 + 16t + c16, this lane's 32 bytes (dims 16j..16j+15);
-    // V: rows p0 + 8it + (lane >> 3), bytes 16*(lane & 7) -- 1 KiB per instruction
-    uint4 kr[4][2];
-    lk_u4 vr[8];  // a vector type (not the uint4 struct): held in registers, not in scratch
-    if (tile_live) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const uint32_t p = p0 + 16u * t + 4u * (c16 & 3) + (c16 >> 2);  // MFMA row c16
-            const uint4* src = (const uint4*)(K + (size_t)(p < ctx ? p : plast) * LK_HD + 16 * j);
-            kr[t][0] = src[0];
-            kr[t][1] = src[1];
-        }
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const uint32_t p = p0 + 8u * it + ((uint32_t)lane >> 3);
-            vr[it] = *(const lk_u4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
-        }
-    }
     // q of head c16 (zero past G), dims 16j + 4s .. +3 for step s, as f16 hi + lo
     lk_h4 qh[4], ql[4];
     {
@@ -321,12 +423,33 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
             }
         }
     }
+    // running (max, sum) of head c16 and O (lane: heads 4j + i, dim 4 c16 + d)
     float mt = -INFINITY, lt = 0.f;
     lk_f4 o[4];
 #pragma unroll
     for (int d = 0; d < 4; d++) o[d] = lk_f4{0.f, 0.f, 0.f, 0.f};
-    if (tile_live) {
-        uint16_t* vw = vs[w];
+    uint16_t* vw = vs[w];
+    for (uint32_t tt = 0; tt < T && (uint32_t)w < A; tt++) {
+        const uint32_t p0 = c0 + ((uint32_t)w + A * tt) * 64;
+        if (p0 >= ctx) break;  // wave-uniform
+        // K: sub-tile t rows p0 + 16t + c16, this lane's 32 bytes (dims 16j..16j+15);
+        // V: rows p0 + 8it + (lane >> 3), bytes 16*(lane & 7) -- 1 KiB per instruction
+        uint4 kr[4][2];
+        lk_u4 vr[8];  // a vector type (not the uint4 struct): held in registers, not in scratch
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t p = p0 + 16u * t + 4u * (c16 & 3) + (c16 >> 2);  // MFMA row c16
+            const uint4* src = (const uint4*)(K + (size_t)(p < ctx ? p : plast) * LK_HD + 16 * j);
+            kr[t][0] = src[0];
+            kr[t][1] = src[1];
+        }
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const uint32_t p = p0 + 8u * it + ((uint32_t)lane >> 3);
+            vr[it] = *(const lk_u4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the previous tile's V reads are done
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int it = 0; it < 8; it++)
             *(lk_u4*)&vw[(8 * it + (lane >> 3)) * LK_VS + 8 * (lane & 7)] = vr[it];
@@ -345,7 +468,7 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
             }
             sc[t] = acc;  // lane: positions p0 + 16t + 4j + i, head c16
         }
-        // ---- softmax over the wave's 64 positions, per head (lanes c16, +16, +32, +48)
+        // ---- softmax over the tile's 64 positions, per head (lanes c16, +16, +32, +48)
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -358,13 +481,15 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(mt, mx);    // finite: the tile holds a live position
+        const float fo = expf(mt - mn);    // the running sums' factor (0 on the first tile)
         float sum = 0.f;
         lk_h4 ph[4], pl[4];
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float pe = expf(sc[t][i] - mx);  // 0 for masked positions
+                const float pe = expf(sc[t][i] - mn);  // 0 for masked positions
                 sum += pe;
                 const _Float16 hi = (_Float16)pe;
                 ph[t][i] = hi;
@@ -372,8 +497,15 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
             }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
-        mt = mx;
-        lt = sum;
+        lt = fmaf(lt, fo, sum);
+        mt = mn;
+        // O's heads are 4j + i: their factors live on lanes 4j + i
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float f = __shfl(fo, (int)(4 * j + i), 64);
+#pragma unroll
+            for (int d = 0; d < 4; d++) o[d][i] *= f;
+        }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the V tile is in LDS
         __builtin_amdgcn_wave_barrier();
         // ---- P.V: k = 4j + i <-> position 16t + 4i + j, n = c16 <-> dim 4 c16 + d
@@ -405,106 +537,19 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs 
 #pragma unroll
         for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][4 * c16 + d] = o[d][i];
     __syncthreads();
-
-    // ---- merge the 4 tiles into one partial per query head
-    float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * max_chunks + chunk) * (2 + LK_HD);
-    for (int t = tid; t < G * LK_HD; t += LK_AW * 64) {
-        const int g = t / LK_HD, dd = t % LK_HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < LK_AW; ww++) {
-            if (red_m[ww][g] != -INFINITY) {
-                const float scl = expf(red_m[ww][g] - M);
-                L = fmaf(scl, red_l[ww][g], L);
-                A = fmaf(scl, red_acc[ww][g][dd], A);
-            }
-        }
-        float* ph = part + (size_t)g * max_chunks * (2 + LK_HD);
-        if (dd == 0) {
-            ph[0] = M;
-            ph[1] = L;
-        }
-        ph[2 + dd] = A;
-    }
+    write_chunk_partial<G>(a, seq, kvh, chunk, red_m, red_l, red_acc);
+    count_in_and_fold<G>(a, seq, kvh, nch);
 }
 
-// Fold the chunk partials of one query head: out = sum_c e^{m_c-M} acc_c /
-// sum_c e^{m_c-M} l_c.  Four waves take interleaved quarters of the chunks
-// (lane = dim; 32 chunks' words in flight per lane, so contexts up to 32768
-// positions take one memory round trip), each folding online against its own
-// running max, and combine their (m, l, acc) in LDS.
-__global__ __launch_bounds__(256) void attn_merge_kernel(const LkAttnArgs a) {
-    const uint32_t h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x & 63;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t ctx = attn_ctx(a, seq);
-    const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
-    const uint32_t nch = (ctx + LK_ACHUNK - 1) / LK_ACHUNK;
-    const float* part = a.part + ((size_t)seq * a.n_heads + h) * max_chunks * (2 + LK_HD);
-    __shared__ float wm[4], wl[4], wa[4][LK_HD];
-    float M = -INFINITY, L = 0.f, A = 0.f;
-    for (uint32_t c0 = w * LK_MB; c0 < nch; c0 += 4 * LK_MB) {  // this wave's next LK_MB chunks
-        // (m, l) by vector loads: lane k < 32 holds chunk c0+k's m, lane
-        // 32+k its l (uniform-address scalar loads would queue behind the
-        // scalar unit's few outstanding requests)
-        const uint32_t kk = lane & 31;
-        const bool live = c0 + kk < nch;
-        const float ml = live ? part[(size_t)(c0 + kk) * (2 + LK_HD) + (lane >> 5)] : (lane < 32 ? -INFINITY : 0.f);
-        float av[LK_MB];
-#pragma unroll
-        for (int k = 0; k < LK_MB; k++) {
-            const uint32_t c = c0 + k < nch ? c0 + k : c0;  // in-range reload, dropped below
-            av[k] = part[(size_t)c * (2 + LK_HD) + 2 + lane];
-        }
-        float mx = lane < 32 ? ml : -INFINITY;
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        const float Mn = fmaxf(M, __shfl(mx, 0, 64));
-        const float rs = expf(M - Mn);  // 0 while M is still -inf
-        // lane k < 32: chunk k's weight e^{m_k - Mn} (0 for dead chunks)
-        const float sck = lane < 32 && live ? expf(ml - Mn) : 0.f;
-        const float lk = __shfl(ml, (int)kk + 32, 64);  // chunk kk's l
-        float ls = lane < 32 ? sck * lk : 0.f;
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
-        L = fmaf(L, rs, __shfl(ls, 0, 64));
-        A *= rs;
-#pragma unroll
-        for (int k = 0; k < LK_MB; k++) {
-            const float sk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sck), k));
-            A = fmaf(sk, av[k], A);
-        }
-        M = Mn;
-    }
-    if (lane == 0) {
-        wm[w] = M;
-        wl[w] = L;
-    }
-    wa[w][lane] = A;
-    __syncthreads();
-    if (w != 0) return;
-    float Mt = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; i++) Mt = fmaxf(Mt, wm[i]);
-    float Lt = 0.f, At = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (wm[i] != -INFINITY) {  // a wave with no chunks holds nothing
-            const float sc = expf(wm[i] - Mt);
-            Lt = fmaf(sc, wl[i], Lt);
-            At = fmaf(sc, wa[i][lane], At);
-        }
-    }
-    a.out[((size_t)seq * a.n_heads + h) * LK_HD + lane] = At / Lt;
-}
-
-hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
-    if (a.n_kv == 0 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
+hipError_t lk_attn_launch(const LkAttnArgs& args, hipStream_t st) {
+    if (args.n_kv == 0 || args.n_heads % args.n_kv || !args.cnt || !args.max_seq) return hipErrorInvalidValue;
+    LkAttnArgs a = args;
+    const AttnPlan p = attn_plan(a.n_seq, a.n_kv, a.max_seq);
+    a.waves = p.waves;
+    a.tiles = p.tiles;
+    a.cstride = attn_chunk_cap(a.max_seq);
     const uint32_t G = a.n_heads / a.n_kv;
-    const uint32_t max_chunks = (a.max_seq + LK_ACHUNK - 1) / LK_ACHUNK;
-    dim3 grid(max_chunks, a.n_kv, a.n_seq);
+    dim3 grid(p.chunks, a.n_kv, a.n_seq);
     // The matrix-core kernel is the faster one at every context measured (4
     // sequences x 24 layers: 268 vs 327 us per step at ctx 4096, 562 vs 690
     // at 32768); LKHIP_ATTN=valu selects the vector-ALU kernel.
@@ -528,8 +573,5 @@ hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st) {
     default: return hipErrorInvalidValue;
     }
 #undef LK_ATTN_CASE
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.n_seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }

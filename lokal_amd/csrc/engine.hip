@@ -700,12 +700,12 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             a.v = vc;
             a.kv_f32 = (uint32_t)s->kv_f32;
             a.out = s->att.as<float>();
-            a.part = s->part.as<float>();
             a.st = state;
             a.n_seq = 1;
             a.n_heads = c.num_attention_heads;
             a.n_kv = c.num_key_value_heads;
             a.max_seq = (uint32_t)s->kv_seq;
+            lk_attn_bind_scratch(a, s->part.as<float>(), c.num_key_value_heads);
             a.seq_stride = 0;
             a.q_stride = e->qd;
             STEP(lk_attn_launch(a, st), C_ATTN, 0);
@@ -781,7 +781,8 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         (rc = dev_alloc(s->inner, (size_t)c.intermediate_size * 4)) ||
         (rc = dev_alloc(s->logits, (size_t)c.vocab_size * 4)))
         return rc;
-    if ((rc = dev_alloc(s->part, lk_attn_part_floats(1, c.num_attention_heads, (uint32_t)s->kv_seq) * 4))) return rc;
+    if ((rc = dev_alloc(s->part, lk_attn_scratch_floats(1, c.num_attention_heads, (uint32_t)s->kv_seq,
+                                                           c.num_key_value_heads) * 4))) return rc;
     s->head_blocks = lk_lm_head_blocks(c.vocab_size, e->lm_head->dw.type, c.hidden_size);
     if ((rc = dev_alloc(s->keys, (size_t)LK_HEAD_MAX_BLOCKS * 2 * 8)) || (rc = dev_alloc(s->head_epoch, 4)) ||
         (rc = dev_alloc(s->err, 4)))
@@ -1106,7 +1107,7 @@ static int rows_alloc(const lkhip_engine* e, Rows& R, uint32_t cap, uint32_t max
         (rc = dev_alloc(R.logits, lrows * c.vocab_size * 4)) ||
         (rc = dev_alloc(R.keys, lrows * ((c.vocab_size + LK_ARGMAX_SLICE - 1) / LK_ARGMAX_SLICE) * 8)) ||
         (rc = dev_alloc(R.gpart, rows_gemm_part(e, cap) * 4)) ||
-        (rc = dev_alloc(R.apart, lk_attn_part_floats(cap, c.num_attention_heads, max_seq) * 4)))
+        (rc = dev_alloc(R.apart, lk_attn_scratch_floats(cap, c.num_attention_heads, max_seq, (size_t)cap * c.num_key_value_heads) * 4)))
         return rc;
     HIP_OR_FAIL(hipHostMalloc((void**)&R.h_meta, 5 * (size_t)cap * 4, hipHostMallocDefault));
     return LKHIP_OK;
@@ -1209,13 +1210,13 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.v = vc;
             a.kv_f32 = (uint32_t)kv.kv_f32;
             a.out = att;
-            a.part = R.apart.as<float>();
             a.ctx_len = ctx;
             a.slots = slots;
             a.n_seq = n;
             a.n_heads = c.num_attention_heads;
             a.n_kv = c.num_key_value_heads;
             a.max_seq = kv.kv_seq;
+            lk_attn_bind_scratch(a, R.apart.as<float>(), (size_t)R.cap * c.num_key_value_heads);
             a.seq_stride = kv.slot_elems;
             a.q_stride = qkvd;
             RSTEP(lk_attn_launch(a, st));
@@ -1889,19 +1890,19 @@ static int attn_decode_check(const float* q, const uint16_t* k_cache, const uint
 }
 
 static int attn_decode_launch(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
-                              size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t max_seq, float* out, float* part,
-                              void* stream) {
+                              size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t max_seq, float* out, float* buf,
+                              size_t cnt_cap, void* stream) {
     LkAttnArgs a{};
     a.q = q;
     a.k = k_cache;
     a.v = v_cache;
     a.out = out;
-    a.part = part;
     a.ctx_len = ctx_len;
     a.n_seq = (uint32_t)n_seq;
     a.n_heads = (uint32_t)n_heads;
     a.n_kv = (uint32_t)n_kv_heads;
     a.max_seq = (uint32_t)max_seq;
+    lk_attn_bind_scratch(a, buf, cnt_cap);
     a.seq_stride = (uint64_t)n_kv_heads * max_seq * 64;
     a.q_stride = n_heads * 64;
     LAUNCH_OR_FAIL(lk_attn_launch(a, (hipStream_t)stream));
@@ -1914,25 +1915,32 @@ extern "C" int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const 
     int rc = attn_decode_check(q, k_cache, v_cache, ctx_len, n_heads, n_kv_heads, head_dim, out, "attn_decode");
     if (rc) return rc;
     if (n_seq == 0 || max_seq == 0) return LKHIP_OK;
-    // Partial buffer for this call, cached per thread and grown on demand.
-    // (Deliberately never freed at thread exit: the HIP runtime may already be
-    // torn down by then.)
-    static thread_local void* part = nullptr;
-    static thread_local size_t part_bytes = 0;
-    const size_t need = lk_attn_part_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq) * 4;
-    if (need > part_bytes) {
+    if (n_seq > 0xFFFFFFFFu || max_seq > 0x7FFFFFFFu)
+        return fail(LKHIP_E_INVALID, "attn_decode: n_seq or max_seq out of range");
+    // Scratch for this call (arrival counters + partials), cached per thread
+    // and grown on demand; a new buffer starts zeroed.  (Deliberately never
+    // freed at thread exit: the HIP runtime may already be torn down by then.)
+    static thread_local void* buf = nullptr;
+    static thread_local size_t buf_bytes = 0, cnt_cap = 0;
+    const size_t cnt_need = n_seq * n_kv_heads;
+    const size_t part_need = lk_attn_part_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq);
+    if (cnt_need > cnt_cap || (lk_attn_cnt_region(cnt_cap) + part_need) * 4 > buf_bytes) {
+        const size_t cap = std::max<size_t>({cnt_cap, cnt_need, 256});
+        const size_t need = (lk_attn_cnt_region(cap) + part_need) * 4;
         HIP_OR_FAIL(hipStreamSynchronize((hipStream_t)stream));
-        if (part) (void)hipFree(part);
-        part = nullptr;
-        part_bytes = 0;
-        if (hipMalloc(&part, need) != hipSuccess) {
-            part = nullptr;
+        if (buf) (void)hipFree(buf);
+        buf = nullptr;
+        buf_bytes = cnt_cap = 0;
+        if (hipMalloc(&buf, need) != hipSuccess) {
+            buf = nullptr;
             return fail(LKHIP_E_NOMEM, "hipMalloc of %zu bytes failed", need);
         }
-        part_bytes = need;
+        HIP_OR_FAIL(hipMemset(buf, 0, need));
+        buf_bytes = need;
+        cnt_cap = cap;
     }
-    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, (float*)part,
-                              stream);
+    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, (float*)buf,
+                              cnt_cap, stream);
 }
 
 extern "C" int lkhip_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -1944,15 +1952,22 @@ extern "C" int lkhip_attn_decode_noalloc(const float* q, const uint16_t* k_cache
     if (n_seq == 0 || max_seq == 0) return LKHIP_OK;
     if (n_seq > 0xFFFFFFFFu || max_seq > 0x7FFFFFFFu)
         return fail(LKHIP_E_INVALID, "attn_decode_noalloc: n_seq or max_seq out of range");
-    const size_t need = lk_attn_part_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq);
+    if (n_seq * n_kv_heads > LK_ATTN_SCRATCH_CNT)
+        return fail(LKHIP_E_INVALID,
+                    "attn_decode_noalloc: %zu sequences x %zu kv heads exceed its %u arrival counters — use "
+                    "lkhip_attn_decode",
+                    n_seq, n_kv_heads, LK_ATTN_SCRATCH_CNT);
+    const size_t need = lk_attn_scratch_floats((uint32_t)n_seq, (uint32_t)n_heads, (uint32_t)max_seq,
+                                               LK_ATTN_SCRATCH_CNT);
     if (need > LK_ATTN_SCRATCH_FLOATS)
         return fail(LKHIP_E_INVALID,
-                    "attn_decode_noalloc: %zu sequences x %zu heads x %zu positions need %zu partial floats, more "
+                    "attn_decode_noalloc: %zu sequences x %zu heads x %zu positions need %zu scratch floats, more "
                     "than its fixed %u-float (8 MiB) device buffer — use lkhip_attn_decode",
                     n_seq, n_heads, max_seq, need, LK_ATTN_SCRATCH_FLOATS);
-    float* part = nullptr;
-    HIP_OR_FAIL(lk_attn_scratch(&part));
-    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, part, stream);
+    float* buf = nullptr;
+    HIP_OR_FAIL(lk_attn_scratch(&buf));
+    return attn_decode_launch(q, k_cache, v_cache, ctx_len, n_seq, n_heads, n_kv_heads, max_seq, out, buf,
+                              LK_ATTN_SCRATCH_CNT, stream);
 }
 
 extern "C" int lkhip_argmax(const float* x, size_t n_rows, size_t n, uint32_t* out, void* stream) {

@@ -189,16 +189,36 @@ struct LkAttnArgs {
     const void* v;
     float* out;
     float* part;            // scratch: [seq][n_heads][max_chunks][2 + 64]
+    uint32_t* cnt;          // [seq][n_kv] chunk arrival counters, zero between launches
     const uint32_t* ctx_len;
     const LkStepState* st;  // decode step state (single sequence, graph mode)
     const uint32_t* slots;  // optional row -> cache slot map
     uint32_t n_seq, n_heads, n_kv, max_seq;
     uint64_t seq_stride;    // elements between two slots of the cache
-    uint64_t q_stride;      // floats between two sequences' q (and out) rows
+    uint64_t q_stride;      // floats between two sequences' q rows (out rows are n_heads * 64 apart)
     uint32_t kv_f32;        // 1: the cache holds f32, 0: f16
+    uint32_t waves, tiles, cstride;  // set by lk_attn_launch: its chunk plan and partial slots per head
 };
 uint32_t lk_attn_chunk(uint32_t max_seq);
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);
+// A launch's scratch buffer: a region of cnt_cap arrival counters (u32,
+// one per (sequence, kv head), n_seq * n_kv <= cnt_cap) that must be zero
+// before the buffer's first launch -- every launch leaves them zero -- then
+// the partials.  The counters sit at a fixed place whatever the shape, so
+// launches of different shapes on one buffer never see a partial as a count.
+#ifndef LK_ATTN_CNT_STRIDE
+#define LK_ATTN_CNT_STRIDE 64u  // words between two counters: each in its own 256-byte line
+#endif
+inline size_t lk_attn_cnt_region(size_t cnt_cap) { return cnt_cap * LK_ATTN_CNT_STRIDE; }
+inline size_t lk_attn_scratch_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq, size_t cnt_cap) {
+    return lk_attn_cnt_region(cnt_cap) + lk_attn_part_floats(n_seq, n_heads, max_seq);
+}
+inline void lk_attn_bind_scratch(LkAttnArgs& a, float* buf, size_t cnt_cap) {
+    a.cnt = (uint32_t*)buf;
+    a.part = buf + lk_attn_cnt_region(cnt_cap);
+}
+// Counter words reserved in the no-allocation entry point's fixed buffer.
+#define LK_ATTN_SCRATCH_CNT 1024u
 hipError_t lk_attn_launch(const LkAttnArgs& a, hipStream_t st);
 // The fixed partial buffer of the no-allocation attention entry point:
 // LK_ATTN_SCRATCH_FLOATS floats (8 MiB) per device; lk_attn_scratch gives

@@ -28,7 +28,7 @@ Prints one JSON object per measurement:
   mix     a short run of every decode-step kernel family, for profiler
           counter passes (rocprofv3 --pmc): 8 greedy tokens of config 3
           (fused_step_kernel, lm_head_kernel), one config-5 step of 24
-          layers at 4096 positions (attn_mfma_kernel, attn_merge_kernel), 8
+          layers at 4096 positions (attn_mfma_kernel), 8
           batched greedy steps of 4 rows (fused_rows_kernel);
   batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
           with a 512-token prompt, then 64 greedy steps of all B rows on the
@@ -207,10 +207,16 @@ def attn() -> list[dict]:
                 K.attn_decode(q, k, v, cl, n_seq, nh, nkv, hd, ctx, o, st.ptr)
 
         ms = _timed(step, 10, st)
+        # the same 24 launches captured into a HIP graph, 4 steps' worth
+        layer_fns = [(lambda k=k, v=v: K.attn_decode(q, k, v, cl, n_seq, nh, nkv, hd, ctx, o, st.ptr))
+                     for k, v in caches]
+        gms = _timed_graph_seq(layer_fns, 4, st) * n_layers
         nbytes = n_layers * n_seq * nkv * ctx * hd * 2 * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
+        ggbs = nbytes / (gms * 1e-3) / 1e9
         out.append({"workload": "attn-4seq", "ctx": ctx, "layers": n_layers, "us_per_step": round(ms * 1e3, 1),
-                    "kv_bytes_per_step": nbytes, "gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+                    "us_per_step_graph": round(gms * 1e3, 1), "kv_bytes_per_step": nbytes, "gbs": round(gbs, 1),
+                    "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4), "frac_of_hbm_graph": round(ggbs / HBM_PEAK_GBS, 4)})
         for k, v in caches:
             k.free()
             v.free()

@@ -232,12 +232,24 @@ def test_attention_config5_four_sequences_32k():
 
 
 def test_attention_merge_boundary_and_repeat():
-    """Contexts on both sides of 32 chunks (8192 positions: one fold round
-    per merge wave) in one call, repeated on the same cached partial buffer
-    with other shapes in between."""
+    """Contexts on both sides of 8192 positions in one call, repeated on the
+    same cached scratch buffer with other shapes in between."""
     for rep in range(3):
         _attn_case(3, 14, 2, [8192, 8193, 8191], 8448, seed=21 + rep)
         _attn_case(2, 14, 2, [8192, 256], 8192, seed=31 + rep)
+
+
+def test_attention_chunk_plans():
+    """Each chunk plan of the launch (A active waves of 8 per block, T tiles
+    per wave, at most 32 chunks per sequence and kv head): A = 8 with T = 1
+    and 2, A = 4, A = 2 with T = 3, A = 1, on ragged contexts; then the
+    first shape again on the same scratch buffer."""
+    _attn_case(4, 14, 2, [16384, 16383, 1, 300], 16384, seed=51)      # A=8, T=1
+    _attn_case(4, 14, 2, [32768, 20000, 16385, 64], 32768, seed=52)   # A=8, T=2
+    _attn_case(4, 14, 2, [4096, 4000, 129, 65], 4096, seed=53)        # A=4, T=1
+    _attn_case(3, 14, 2, [8448, 8192, 4097], 8448, seed=54)           # A=2, T=3
+    _attn_case(1, 14, 2, [1000], 1024, seed=55)                       # A=1, T=1
+    _attn_case(4, 14, 2, [16384, 16383, 1, 300], 16384, seed=51)
 
 
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])

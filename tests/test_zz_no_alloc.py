@@ -14,6 +14,7 @@ from lokal_amd import kernels as K
 
 TOL = 1e-3
 SCRATCH_FLOATS = 2 << 20
+CNT_WORDS = 1024 * 64  # 1024 counters, one per 256-byte line
 
 
 def rel_err(a, b):
@@ -58,15 +59,28 @@ def test_noalloc_matches_allocating_entry_point_twice():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def _scratch_floats(n_seq, nh, max_seq):
+    """Floats the call needs: 1024 counters 64 words apart, then per
+    (sequence, head) min(32, ceil(max_seq / 64)) chunk slots of 2 + 64 floats."""
+    return CNT_WORDS + n_seq * nh * min(32, -(-max_seq // 64)) * 66
+
+
 def test_noalloc_refuses_more_than_its_buffer():
-    """The size check runs on the host before any device work (no GPU needed):
-    8 sequences x 32 heads x 32768 positions need 8*32*128*66 floats > 2^21."""
+    """The size checks run on the host before any device work (no GPU
+    needed).  The pointers are dummies, so the sizes are first checked here
+    to be refused: a call that passed the checks would launch on them."""
     L = _lib.lib()
     dummy = C.c_void_p(256)
-    rc = L.lkhip_attn_decode_noalloc(dummy, dummy, dummy, dummy, 8, 32, 4, 64, 32768, dummy, None)
+    # 64 sequences x 32 heads x 32768 positions: 64*32*32*66 partial floats > 2^21
+    assert _scratch_floats(64, 32, 32768) > SCRATCH_FLOATS >= _scratch_floats(4, 14, 32768)
+    rc = L.lkhip_attn_decode_noalloc(dummy, dummy, dummy, dummy, 64, 32, 4, 64, 32768, dummy, None)
     assert rc == -1
     msg = L.lkhip_last_error().decode()
     assert "lkhip_attn_decode" in msg and "8 MiB" in msg
-    assert 8 * 32 * 128 * 66 > SCRATCH_FLOATS >= 4 * 14 * 128 * 66
+    # 512 sequences x 4 kv heads need more than the 1024 arrival counters
+    assert _scratch_floats(512, 8, 64) <= SCRATCH_FLOATS
+    rc = L.lkhip_attn_decode_noalloc(dummy, dummy, dummy, dummy, 512, 8, 4, 64, 64, dummy, None)
+    assert rc == -1
+    assert "arrival counters" in L.lkhip_last_error().decode()
     # a zero-size call is a no-op, like the allocating entry point
     assert L.lkhip_attn_decode_noalloc(dummy, dummy, dummy, dummy, 0, 14, 2, 64, 1024, dummy, None) == 0
