@@ -342,13 +342,13 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "wider or deeper than the one-kernel step takes";
         return LKHIP_OK;
     }
-    if (c.num_attention_heads * ((LK_FUSED_MAX_SEQ + 63) / 64) > nw) {
+    if (c.num_attention_heads * LK_FUSED_MAX_CH > nw) {
         e->fused_why = "more attention tiles than waves";
         return LKHIP_OK;
     }
     // LDS limit for the longest session the one-kernel step serves
     e->fused_lds = lk_fused_lds_bytes(h, I, c.num_attention_heads, c.num_key_value_heads, (uint32_t)e->fused_g,
-                                      (LK_FUSED_MAX_SEQ + 63) / 64);
+                                      LK_FUSED_MAX_CH);
     LkFusedArgs probe{};
     hipError_t st = hipSuccess;
     for (int kv32 = 0; kv32 < 2 && st == hipSuccess; kv32++)  // both KV cache types
@@ -792,7 +792,7 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
     if (e->fused_ok && max_seq <= LK_FUSED_MAX_SEQ) {
         const size_t h = c.hidden_size, I = c.intermediate_size;
         const size_t qkvd = e->qd + 2 * e->kvd;
-        s->max_chunks = (uint32_t)((max_seq + 63) / 64);
+        s->max_chunks = (uint32_t)std::min<size_t>((max_seq + 63) / 64, LK_FUSED_MAX_CH);
         if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
             (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * s->max_chunks * 66 * 8)) ||
             (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
@@ -1570,7 +1570,7 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
     // the multi-row one-kernel step, where the model's shape has one
     // (LKHIP_BATCH_FUSED=0 keeps every step on the per-layer launches)
     const char* fe = getenv("LKHIP_BATCH_FUSED");
-    if (e->fused_ok && !(fe && fe[0] == '0') && kv_seq <= LK_FUSED_MAX_SEQ) {
+    if (e->fused_ok && !(fe && fe[0] == '0') && kv_seq <= LK_FUSED_ROWS_MAX_SEQ) {
         const size_t h = c.hidden_size, I = c.intermediate_size, nb = LK_FUSED_ROWS;
         const size_t qkvd = e->qd + 2 * e->kvd;
         b->fused_chunks = (uint32_t)(kv_seq / 64);

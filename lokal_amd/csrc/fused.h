@@ -59,8 +59,13 @@ __host__ __device__ inline uint32_t lk_fused_trace_len(uint32_t n_layers) { retu
 // LDS of one workgroup for sessions of up to max_chunks 64-position tiles.
 size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks);
 // Longest session (positions) the one-kernel step serves; longer ones run the
-// per-stage kernels (their attention partials would not fit in LDS).
-#define LK_FUSED_MAX_SEQ 4096u
+// per-stage kernels.  A head's attention is split into at most
+// LK_FUSED_MAX_CH chunks of whole 64-position tiles (one per lane of the
+// merge), each chunk one wave.
+#define LK_FUSED_MAX_SEQ 32768u
+#define LK_FUSED_MAX_CH 64u
+// Longest session of the multi-row one-kernel step (one tile per wave).
+#define LK_FUSED_ROWS_MAX_SEQ 4096u
 // Waves per workgroup.
 #define LK_FUSED_WAVES 8u
 

@@ -21,8 +21,9 @@
 //               k/v rounded to the cache type, written to the KV cache and
 //               published for this token's attention
 //   S2 attn     one wave per (query head, chunk of 64-position tiles), spread
-//               over the whole grid: K/V of cached positions loaded before the
-//               wait for q; online softmax; one (m, l, acc[64]) partial each
+//               over the whole grid: K/V of the chunk's first tile loaded
+//               before the wait for q; online softmax across the chunk's
+//               tiles; one (m, l, acc[64]) partial each
 //   S3 merge    one wave per query head folds its chunks -> attention output
 //   S4 o_proj   o_proj + residual -> x'
 //   S5 gate/up  RMSNorm(x') + SwiGLU  -> inner
@@ -104,9 +105,12 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     const uint32_t nL = a.n_layers;
     const float fpos = (float)pos;
     const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
-    // attention items: (query head, 64-position tile), one wave each
-    const uint32_t nch = ntile;          // partials per head
-    const uint32_t nps = a.max_chunks;   // partial slots per head
+    // attention items: (query head, chunk of tpw consecutive tiles), one wave
+    // each; tpw grows with the context so a head never has more than
+    // LK_FUSED_MAX_CH chunks (S3 holds one chunk per lane)
+    const uint32_t tpw = (ntile + LK_FUSED_MAX_CH - 1) / LK_FUSED_MAX_CH;
+    const uint32_t nch = (ntile + tpw - 1) / tpw;  // partials per head
+    const uint32_t nps = a.max_chunks;             // partial slots per head
 
     // S1 work of this wave: q/k/v rows (i, i+32) of one head
     const uint32_t U1 = (nh + 2 * nkv) * 32;
@@ -258,39 +262,40 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         };
         if (c.gw >= (int)(nh * nch)) issue_ahead();
         LKF_MARK(2 + 6 * L + 0);
-        // ---------------- S2: attention partials.  Item = (query head, tile of
-        // 64 positions), one wave each, spread over the grid (items past the
-        // first half's waves, at long contexts, go to the second half): the
-        // wave scores its 64 positions (lane = position), takes the tile's
-        // softmax max and sum, and accumulates P.V with lane = (position
-        // group lane & 7, dims 8 * (lane >> 3) ..+7).
+        // ---------------- S2: attention partials.  Item = (query head, chunk
+        // of tpw tiles of 64 positions), one wave each, spread over the grid
+        // (items past the first half's waves, at long contexts, go to the
+        // second half): per tile the wave scores its 64 positions (lane =
+        // position), folds the tile's max and sum into its running softmax,
+        // and accumulates P.V with lane = (position group lane & 7, dims
+        // 8 * (lane >> 3) ..+7).
         if (c.gw < (int)(nh * nch)) {
             const uint32_t hq = (uint32_t)c.gw / nch, ck = (uint32_t)c.gw % nch;
             const uint32_t j = hq / G;
-            const uint32_t t = ck;
-            const bool has_cur = t + 1 == ntile;  // the tile holding position pos
+            const uint32_t t0 = ck * tpw, t1 = t0 + tpw < ntile ? t0 + tpw : ntile;
+            const bool chunk_cur = t1 == ntile;  // the chunk holding position pos
             LKF_SUB(0);
             const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
             const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
             const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
-            // Cached positions (< pos) do not depend on this token: load them
-            // first.  The cache holds whole 64-position tiles (its per-head
-            // stride is max_seq rounded up to 64), so every row of the tile is
-            // in bounds; rows >= pos are replaced (pos) or masked (> pos) below.
-            // One base address per lane, the rest immediate offsets.
+            // Cached positions (< pos) do not depend on this token: the first
+            // tile is loaded before the wait for q.  The cache holds whole
+            // 64-position tiles (its per-head stride is max_seq rounded up to
+            // 64), so every row of a tile is in bounds; rows >= pos are
+            // replaced (pos) or masked (> pos) below.
             uint4 kraw[KC], vraw[KC];
             // K rows from pos on are this token's (in flight from S1) or
             // unwritten: read row pos - 1 instead (the lane's score is
             // replaced or masked below)
-            uint32_t krow = t * 64u + (uint32_t)lane;
-            krow = krow < pos ? krow : (pos ? pos - 1 : 0);
-            const KV* Kl = K + krow * 64u;
-            const KV* Vl = V + (t * 64u + sub) * 64u + dq;
-            auto load_k = [&](uint32_t) {
+            auto load_k = [&](uint32_t t) {
+                uint32_t krow = t * 64u + (uint32_t)lane;
+                krow = krow < pos ? krow : (pos ? pos - 1 : 0);
+                const KV* Kl = K + krow * 64u;
 #pragma unroll
                 for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
             };
-            auto load_v = [&](uint32_t) {
+            auto load_v = [&](uint32_t t) {
+                const KV* Vl = V + (t * 64u + sub) * 64u + dq;
 #pragma unroll
                 for (int q = 0; q < KC; q++)
                     vraw[q] = *(const uint4*)(Vl + (KV32 ? (q / 2) * 8 * 64 + (q & 1) * 4 : q * 8 * 64));
@@ -300,7 +305,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 load_k(t);
                 if constexpr (!KV32) load_v(t);
             };
-            load_tile(t);
+            load_tile(t0);
             issue_ahead();
             LKF_SUB(1);
             {  // this head's q; this token's k and v for the chunk that holds pos
@@ -308,10 +313,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 const uint64_t* sk = QB + qd + j * 64 + lane;
                 const uint64_t* sv = QB + qd + kvd + j * 64 + lane;
                 const uint64_t w0 = ld_word(sq);
-                const uint64_t w1 = has_cur ? ld_word(sk) : 0;
-                const uint64_t w2 = has_cur ? ld_word(sv) : 0;
+                const uint64_t w1 = chunk_cur ? ld_word(sk) : 0;
+                const uint64_t w2 = chunk_cur ? ld_word(sv) : 0;
                 wq[lane] = (uint32_t)(w0 >> 32) == ep ? __uint_as_float((uint32_t)w0) : await(c, sq, ep);
-                if (has_cur) {
+                if (chunk_cur) {
                     wk[lane] = (uint32_t)(w1 >> 32) == ep ? __uint_as_float((uint32_t)w1) : await(c, sk, ep);
                     wvc[lane] = (uint32_t)(w2 >> 32) == ep ? __uint_as_float((uint32_t)w2) : await(c, sv, ep);
                 }
@@ -321,8 +326,13 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             float acc[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[e] = 0.f;
-            float m, l;
-            {
+            float m = -INFINITY, l = 0.f;
+            for (uint32_t t = t0; t < t1; t++) {
+                if (t > t0) {
+                    wave_sync_lds();  // the previous tile's weight reads are done
+                    load_tile(t);
+                }
+                const bool has_cur = t + 1 == ntile;  // the tile holding position pos
                 const uint32_t p = t * 64 + (uint32_t)lane;
                 const bool valid = p <= pos;
                 // this token's k (lane p == pos) comes from LDS: its cache row
@@ -351,12 +361,17 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
                 LKF_SUB(3);
                 if constexpr (KV32) load_v(t);
-                // the tile's part of math::softmax (src/math.rs:55-66); tiles
-                // are combined in S3 with the split-invariant rescaling
+                // the tile's part of math::softmax (src/math.rs:55-66), folded
+                // into the chunk's running max and sum; chunks are combined in
+                // S3 with the same split-invariant rescaling
                 const float sg = valid ? s * 0.125f : -INFINITY;
-                m = lk_wave_max(sg);
-                const float pe = valid ? expf(sg - m) : 0.f;
-                l = lk_wave_sum(pe);
+                const float mn = fmaxf(m, lk_wave_max(sg));  // finite: the tile holds position <= pos
+                const float fo = expf(m - mn);                // 0 on the chunk's first tile
+                const float pe = valid ? expf(sg - mn) : 0.f;
+                l = fmaf(l, fo, lk_wave_sum(pe));
+                m = mn;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] *= fo;
                 wP[(lane & 7) * 8 + (lane >> 3)] = pe;  // [group][jj]: a lane's 8 weights are adjacent
                 wave_sync_lds();
                 LKF_SUB(4);

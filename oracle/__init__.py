@@ -90,6 +90,7 @@ def lib():
         L.oracle_session_hidden.argtypes = [C.c_void_p, F32P]
         L.oracle_session_kv.argtypes = [C.c_void_p, C.c_uint32, C.c_size_t, C.c_int, F32P]
         L.oracle_session_set_kv_f16.argtypes = [C.c_void_p, C.c_int]
+        L.oracle_session_load_kv.argtypes = [C.c_void_p, C.c_uint32, C.c_size_t, C.c_size_t, C.c_int, F32P]
         L.oracle_f32_to_f16.argtypes = [C.c_float]
         L.oracle_f32_to_f16.restype = C.c_uint16
         _lib = L
@@ -280,6 +281,13 @@ class Session:
         out = np.empty(kvd, dtype=np.float32)
         lib().oracle_session_kv(self._s, layer, pos, int(which_v), out)
         return out
+
+    def load_kv(self, layer: int, pos0: int, which_v: bool, rows) -> None:
+        """Overwrite cached rows [pos0, pos0 + len(rows)) of one layer (test
+        helper: continue from a cache another implementation filled)."""
+        rows = np.ascontiguousarray(rows, dtype=np.float32)
+        if lib().oracle_session_load_kv(self._s, layer, pos0, rows.shape[0], int(which_v), rows) != 0:
+            raise ValueError("oracle load_kv: layer or positions out of range")
 
     def close(self):
         if self._s:

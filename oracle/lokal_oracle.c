@@ -621,6 +621,17 @@ ORACLE_API void oracle_session_hidden(const oracle_session* s, float* out) {
     memcpy(out, s->x, s->m->cfg.hidden * sizeof(float));
 }
 
+/* Test-only: overwrite n cached K or V rows of one layer from position pos0
+ * (f32 rows of kv_dim), so that a test can continue a session from a cache
+ * another implementation filled.  No counterpart in lokal. */
+ORACLE_API int oracle_session_load_kv(oracle_session* s, uint32_t layer, size_t pos0, size_t n, int which_v,
+                                      const float* rows) {
+    if (layer >= s->m->cfg.n_layers || pos0 > s->max_seq || n > s->max_seq - pos0) return -1;
+    float* dst = (which_v ? s->v[layer] : s->k[layer]) + pos0 * s->m->kv_dim;
+    memcpy(dst, rows, n * s->m->kv_dim * sizeof(float));
+    return 0;
+}
+
 /* Read one layer's cached K or V row (f32) at position pos. */
 ORACLE_API int oracle_session_kv(const oracle_session* s, uint32_t layer, size_t pos, int which_v, float* out) {
     if (layer >= s->m->cfg.n_layers || pos >= s->max_seq) return -1;

@@ -254,3 +254,35 @@ def test_greedy_64_steps_at_the_configs_prompt_lengths_f32_kv(name, prompt_len):
     step at positions 512..575 (256..319), ids identical to the CPU path's and
     logits within 1e-3, f32 KV caches on both sides (src/generate.rs:80-118)."""
     _greedy_identity(name, "f32", prompt_len=prompt_len, seed=4)
+
+
+@pytest.mark.parametrize("n_prompt,max_seq", [(8200, 8300), (16300, 16400)])
+def test_one_kernel_step_past_4096_positions_matches_oracle_on_the_same_cache(n_prompt, max_seq):
+    """Sessions longer than 4096 positions stay on the one-kernel step, whose
+    attention stage then gives each wave a chunk of several 64-position tiles
+    (at most 64 chunks per head).  The prompt goes through the GPU prefill;
+    the oracle takes the GPU's f16 cache rows, so both continue from the same
+    cache, and four decode steps at positions n_prompt.. must give logits
+    within the f16-cache bar."""
+    cfg, tensors, eng, om = build("q8_0", "fused", seed=12)
+    s = eng.session(max_seq, kv_dtype="f16")
+    s.set_trace(0)  # refused unless the session runs the one-kernel step
+    rng = np.random.default_rng(n_prompt)
+    s.prefill(rng.integers(0, cfg.vocab_size, n_prompt).astype(np.uint32))
+    o = om.session(max_seq, kv_f16=True)
+    for layer in range(cfg.num_hidden_layers):
+        for which_v in (False, True):
+            rows = np.stack([s.read_kv(layer, p, which_v) for p in range(n_prompt)])
+            o.load_kv(layer, 0, which_v, rows)
+    print(f"{n_prompt}: caches loaded", flush=True)
+    for i, t in enumerate(rng.integers(0, cfg.vocab_size, 4)):
+        pos = n_prompt + i
+        got, want = s.forward(int(t), pos), o.forward(int(t), pos)
+        e = rel_err(got, want)
+        print(f"pos {pos}: logits rel err {e:.3g}", flush=True)
+        assert e < TOL_F16_KV, (pos, e)
+    # the step just run was the traced one-kernel step: its end mark is set
+    assert s.trace_ticks()[0, 2 + 6 * cfg.num_hidden_layers] > 0
+    s.close()
+    o.close()
+    eng.close()
