@@ -30,6 +30,8 @@ Prints one JSON object per measurement:
           (fused_step_kernel, lm_head_kernel), one config-5 step of 24
           layers at 4096 positions (attn_mfma_kernel), 8
           batched greedy steps of 4 rows (fused_rows_kernel);
+  stream  the practical read bandwidth: a plain f32 sum and a device copy
+          (ROCm's own kernels through torch) over 145 MB and 1 GiB;
   batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
           with a 512-token prompt, then 64 greedy steps of all B rows on the
           device: aggregate tok/s and weight GB/s (one weight read per step).
@@ -371,6 +373,35 @@ def mix() -> list[dict]:
     return [{"workload": "mix", "done": True}]
 
 
+def stream() -> list[dict]:
+    """The read bandwidth a plain streaming kernel gets on this device: the
+    ROCm library's f32 sum reduction and device copy (through torch, used
+    here only as a reference kernel) over 145 MB (the Qwen lm_head's Q8_0
+    bytes) and 1 GiB -- the practical ceiling the HBM-bound kernels are
+    compared with, beside the 8 TB/s datasheet peak."""
+    import torch
+    out = []
+    for name, nbytes in (("145MB", 144_643_072), ("1GiB", 1 << 30)):
+        x = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+        y = torch.empty_like(x)
+        for op, fn, moved in (("sum", lambda: x.sum(), nbytes), ("copy", lambda: y.copy_(x), 2 * nbytes)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(20):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) / 20 * 1e3
+            out.append({"workload": "stream", "op": op, "bytes": nbytes, "us": round(us, 2),
+                        "gbs": round(moved / (us * 1e-6) / 1e9, 1),
+                        "frac_of_hbm": round(moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del x, y
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default="decode,layers,attn,gemm,prefill,batch,matvec")
@@ -388,7 +419,8 @@ def main() -> int:
     if "attn" in want:
         for r in attn():
             print(json.dumps(r), flush=True)
-    for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch), ("matvec", matvec), ("mix", mix)):
+    for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch), ("matvec", matvec), ("mix", mix),
+                     ("stream", stream)):
         if name in want:
             for r in fn():
                 print(json.dumps(r), flush=True)
