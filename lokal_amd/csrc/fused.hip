@@ -47,6 +47,9 @@
 // TinyLlama Q4_K: 1 + 1 (1493; 3 + 2: 1226).
 #define LKF_KB (WT == LK_Q8_0 ? 2 : 1)
 #define LKF_KA (WT == LK_Q8_0 ? 2 : 1)
+// gate/up units in flight together in S5 beyond the held ones (Qwen2.5 Q8_0:
+// 2 -> 2319 tok/s, 1 -> 2294; TinyLlama Q4_K: 2 spills, 1347 against 1487)
+#define LKF_XU (WT == LK_Q4_K ? 1 : 2)
 // Stage timestamps of every block (thread 0), kept in LDS and copied out at
 // the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
@@ -530,13 +533,28 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
             LKF_SUB(10);
             LKF_SUB(11);
-            for (int uu = (LKF_KA + LKF_KB) * nwh + c.gw; uu < (int)U5; uu += c.nw) {  // wider models
-                Row<WT, NCHH> gr, pr;
-                row_issue(gr, ly.gate, (uint32_t)uu, lane);
-                row_issue(pr, ly.up, (uint32_t)uu, lane);
-                const float gg = lk_wave_sum(row_dot(gr, xin, h, lane));
-                const float up = lk_wave_sum(row_dot(pr, xin, h, lane));
-                if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
+            // wider models: the remaining units, two at a time in flight
+            // (Q4_K: one at a time, the second pair of rows would spill)
+            constexpr int XU = LKF_XU;
+            for (int uu = (LKF_KA + LKF_KB) * nwh + c.gw; uu < (int)U5; uu += XU * c.nw) {
+                Row<WT, NCHH> gr[XU], pr[XU];
+#pragma unroll
+                for (int x = 0; x < XU; x++) {
+                    const int ux = uu + x * c.nw;
+                    if (ux < (int)U5) {  // wave-uniform
+                        row_issue(gr[x], ly.gate, (uint32_t)ux, lane);
+                        row_issue(pr[x], ly.up, (uint32_t)ux, lane);
+                    }
+                }
+#pragma unroll
+                for (int x = 0; x < XU; x++) {
+                    const int ux = uu + x * c.nw;
+                    if (ux < (int)U5) {
+                        const float gg = lk_wave_sum(row_dot(gr[x], xin, h, lane));
+                        const float up = lk_wave_sum(row_dot(pr[x], xin, h, lane));
+                        if (lane == 0) publish(IB + ux, gg / (1.0f + expf(-gg)) * up, ep);
+                    }
+                }
             }
             if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
             if (has1 && L + 1 < nL) issue_qkv(lay[L + 1]);  // the next layer's q/k/v rows

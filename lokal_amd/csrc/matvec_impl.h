@@ -103,6 +103,26 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
     }
 }
 
+// scale_min_k4 for the sub-block pair j = 2g, 2g + 1 (g = 0..3) in
+// straight-line bit-field extracts.  Byte jj = j & 3 sits at bit 8*jj of a
+// scale dword; for j < 4, sc = s0[jj] & 63 and m = s1[jj] & 63; for j >= 4,
+// sc = (s2[jj] & 15) | ((s0[jj] >> 6) << 4) and m = (s2[jj] >> 4) |
+// ((s1[jj] >> 6) << 4).  Both forms are "4 low bits from A | 2 bits from
+// s0 (s1) << 4", with A and the bit offsets chosen by g alone, so a lane
+// whose g is fixed pays two selects and four extracts per value.
+__device__ __forceinline__ void scale_min_k4_pair(uint32_t g, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc0,
+                                                  uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
+    const bool lo = g < 2;
+    const uint32_t sh = 16u * (g & 1u);        // byte jj of j = 2g
+    const uint32_t A = lo ? s0 : s2, B = lo ? s1 : s2;
+    const uint32_t ob = lo ? 0u : 4u, oh = lo ? 4u : 6u;
+    auto bf = [](uint32_t v, uint32_t o, uint32_t n) { return (v >> o) & ((1u << n) - 1u); };
+    sc0 = bf(A, sh, 4) | (bf(s0, sh + oh, 2) << 4);
+    m0 = bf(B, sh + ob, 4) | (bf(s1, sh + oh, 2) << 4);
+    sc1 = bf(A, sh + 8, 4) | (bf(s0, sh + 8 + oh, 2) << 4);
+    m1 = bf(B, sh + 8 + ob, 4) | (bf(s1, sh + 8 + oh, 2) << 4);
+}
+
 // Q4_K: 16 bytes = 16 low nibbles (elements e0..e0+15 of sub-block 2g) and 16
 // high nibbles (e0+32.. of sub-block 2g+1).  Returns
 //   (d1*sum(q_lo x) - m1*sum(x_lo)) + (d2*sum(q_hi x) - m2*sum(x_hi))
@@ -131,12 +151,10 @@ __device__ __forceinline__ float dot_q4k(uint4 q, uint4 hdr, uint32_t k, const f
     }
     const float d = __half2float(__ushort_as_half((uint16_t)(hdr.x & 0xFFFF)));
     const float dmin = __half2float(__ushort_as_half((uint16_t)(hdr.x >> 16)));
-    const uint32_t g = k >> 1;
-    uint32_t sc, m;
-    scale_min_k4(2 * g, hdr.y, hdr.z, hdr.w, sc, m);
-    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
-    scale_min_k4(2 * g + 1, hdr.y, hdr.z, hdr.w, sc, m);
-    const float d2 = __fmul_rn(d, (float)sc), m2 = __fmul_rn(dmin, (float)m);
+    uint32_t sca, ma, scb, mb;
+    scale_min_k4_pair(k >> 1, hdr.y, hdr.z, hdr.w, sca, ma, scb, mb);
+    const float d1 = __fmul_rn(d, (float)sca), m1 = __fmul_rn(dmin, (float)ma);
+    const float d2 = __fmul_rn(d, (float)scb), m2 = __fmul_rn(dmin, (float)mb);
     const float lo_part = __fsub_rn(__fmul_rn(d1, sql), __fmul_rn(m1, sxl));
     const float hi_part = __fsub_rn(__fmul_rn(d2, sqh), __fmul_rn(m2, sxh));
     return lo_part + hi_part;
