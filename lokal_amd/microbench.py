@@ -30,6 +30,9 @@ Prints one JSON object per measurement:
           (fused_step_kernel, lm_head_kernel), one config-5 step of 24
           layers at 4096 positions (attn_mfma_kernel), 8
           batched greedy steps of 4 rows (fused_rows_kernel);
+  trace   the one-kernel step's per-stage times from every workgroup's
+          stage timestamps (config 3, position 528): each stage's duration
+          to its slowest workgroup and the spread of its end over workgroups;
   stream  the practical read bandwidth: a plain f32 sum and a device copy
           (ROCm's own kernels through torch) over 145 MB and 1 GiB;
   batch   config 3 served by the Batcher: B sequences (B = 1, 4, 16, 64), each
@@ -142,6 +145,52 @@ def decode(name: str, prompt_len: int, steps: int) -> dict:
     return {"workload": name, "prompt": prompt_len, "decode_tokens": steps, "tok_s": round(tok_s, 1),
             "ms_per_token": round(dt / steps * 1e3, 4), "weight_bytes_per_token": wbytes,
             "weight_gbs": round(gbs, 1), "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def stage_trace(name: str = "qwen2.5-0.5b-q8_0", prompt_len: int = 512) -> list[dict]:
+    """Per-stage timing of the one-kernel step from every workgroup's stage
+    timestamps (lkhip_session_set_trace): for each stage of each layer, the
+    end time of every one of the grid's workgroups, relative to the end of the
+    previous layer's last workgroup.  Reports, averaged over the layers after
+    the first two, each stage's duration as seen by the slowest workgroup and
+    the spread (max - min) of its end time over workgroups -- the producer
+    skew that the next stage's consumers wait out."""
+    cfg, tensors = synth.synth_named(name, 0)
+    eng = Engine.from_tensors(cfg, tensors)
+    del tensors
+    s = eng.session(prompt_len + 64)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, prompt_len).astype(np.uint32)
+    tok = int(np.argmax(s.prefill(prompt)))
+    ids = s.decode_greedy(tok, prompt_len, 16)
+    s.set_trace(0)
+    s.decode_greedy(int(ids[-1]), prompt_len + 16, 1)
+    t = s.trace_ticks().astype(np.float64)
+    s.close()
+    eng.close()
+    L = cfg.num_hidden_layers
+    u = (t - t[:, 0].min()) / 100.0  # 100 MHz ticks -> us
+    names = ["qkv", "attn", "merge", "o_proj", "gate_up", "down"]
+    dur = np.zeros(6)
+    skew = np.zeros(6)
+    med = np.zeros(6)
+    n = 0
+    for layer in range(2, L):
+        ref = u[:, 2 + 6 * (layer - 1) + 5].max()
+        prev = 0.0
+        for k in range(6):
+            e = u[:, 2 + 6 * layer + k] - ref
+            dur[k] += e.max() - prev
+            skew[k] += e.max() - e.min()
+            med[k] += np.median(e)
+            prev = e.max()
+        n += 1
+    per_layer = (u[:, 2 + 6 * (L - 1) + 5].max() - u[:, 2 + 6 * 0 + 5].max()) / (L - 1)
+    out = [{"workload": "stage-trace", "model": name, "position": prompt_len + 16, "workgroups": int(t.shape[0]),
+            "us_per_layer": round(per_layer, 2)}]
+    for k in range(6):
+        out.append({"workload": "stage-trace", "stage": names[k], "us_slowest_workgroup": round(dur[k] / n, 2),
+                    "end_median_us": round(med[k] / n, 2), "end_skew_us": round(skew[k] / n, 2)})
+    return out
 
 
 def layers() -> list[dict]:
@@ -420,7 +469,7 @@ def main() -> int:
         for r in attn():
             print(json.dumps(r), flush=True)
     for name, fn in (("gemm", gemm), ("prefill", prefill), ("batch", batch), ("matvec", matvec), ("mix", mix),
-                     ("stream", stream)):
+                     ("stream", stream), ("trace", stage_trace)):
         if name in want:
             for r in fn():
                 print(json.dumps(r), flush=True)
