@@ -320,10 +320,33 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
     constexpr uint32_t CE = ChunkTraits<WT>::elems;
     const int lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const uint32_t row_base = wave * R;
     const uint32_t cols = a.cols;
     const uint32_t nchunk = cols / CE;
     const float* __restrict__ x = a.x;
+    uint64_t key = 0;  // LK_MV_ARGMAX: this wave's best (value, row) key
+    // A row in one pass with a small x slice per lane (Q8_0 / Q8_SM up to 2
+    // chunks, F16 up to 4): the slice is read once into registers for every
+    // row group of the wave, instead of from L1/L2 for each group.
+    constexpr bool XREG = (WT == LK_Q8_0 || WT == LK_Q8_SM) ? NCH <= 2 : (WT == LK_F16 ? NCH <= 4 : false);
+    float xr[XREG ? NCH : 1][CE];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const uint32_t c = (uint32_t)lane + 64u * i;
+#pragma unroll
+            for (int e = 0; e < (int)CE; e += 4) {
+                const float4 v = c < nchunk ? *(const float4*)(x + (size_t)c * CE + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xr[i][e] = v.x;
+                xr[i][e + 1] = v.y;
+                xr[i][e + 2] = v.z;
+                xr[i][e + 3] = v.w;
+            }
+        }
+    }
+    // grid-stride over R-row groups: the grid is capped (lk_matvec_plan), so
+    // large matrices keep a chip-filling set of waves that each take several
+    // groups instead of launching one short-lived wave per group
+    for (uint32_t row_base = wave * R; row_base < a.total_rows; row_base += gridDim.x * 4u * R) {
 
     const uint8_t* rp[NR];
     const uint8_t* ap[NR];
@@ -361,32 +384,35 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
     for (int j = 0; j < NR; j++) acc[j] = 0.f;
 
     for (uint32_t base = 0; base < nchunk; base += 64 * NCH) {
+        // Straight-line loads (a chunk past the row end reloads chunk 0, an
+        // invalid row is row 0 of its segment; both are dropped below): a
+        // lane-dependent guard here would pull the scale conversion, and with
+        // it a wait for the loads, into the guarded block row by row.
         uint4 wq[NR][NCH];
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
             const uint32_t c = base + (uint32_t)lane + 64u * i;
+            const uint32_t cc = c < nchunk ? c : 0u;
 #pragma unroll
-            for (int j = 0; j < NR; j++) {
-                if (c < nchunk && rv[j]) wq[j][i] = ld_stream16(rp[j] + 16u * c);
-                else wq[j][i] = make_uint4(0, 0, 0, 0);
-            }
+            for (int j = 0; j < NR; j++) wq[j][i] = ld_stream16(rp[j] + 16u * cc);
         }
         if constexpr (WT == LK_Q8_0) {
-            float dsc[NR][NCH];
+            uint32_t dbits[NR][NCH];  // raw f16 scale bits, converted at use
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
+                const uint32_t cc = c < nchunk ? c : 0u;
 #pragma unroll
-                for (int j = 0; j < NR; j++)
-                    dsc[j][i] = (c < nchunk && rv[j]) ? lk_h2f(((const uint16_t*)ap[j])[c >> 1]) : 0.f;
+                for (int j = 0; j < NR; j++) dbits[j][i] = lk_g((const uint16_t*)ap[j])[cc >> 1];
             }
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
-                if (c < nchunk) {
-                    const float* xc = x + (size_t)c * 16;
+                const float* xc = XREG ? xr[XREG ? i : 0] : x + (size_t)(c < nchunk ? c : 0u) * 16;
 #pragma unroll
-                    for (int j = 0; j < NR; j++) acc[j] = fmaf(dsc[j][i], dot_q8(wq[j][i], xc), acc[j]);
+                for (int j = 0; j < NR; j++) {
+                    const float t = fmaf(lk_h2f((uint16_t)dbits[j][i]), dot_q8(wq[j][i], xc), acc[j]);
+                    acc[j] = c < nchunk ? t : acc[j];
                 }
             }
         } else if constexpr (WT == LK_Q8_SM) {
@@ -395,26 +421,27 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
 #pragma unroll
-                for (int j = 0; j < NR; j++)
-                    sm[j][i] = (c < nchunk && rv[j]) ? ld_sm(ap[j], c) : make_uint2(0, 0);
+                for (int j = 0; j < NR; j++) sm[j][i] = ld_sm(ap[j], c < nchunk ? c : 0u);
             }
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
-                if (c < nchunk) {
-                    const float* xc = x + (size_t)c * 16;
+                const float* xc = XREG ? xr[XREG ? i : 0] : x + (size_t)(c < nchunk ? c : 0u) * 16;
 #pragma unroll
-                    for (int j = 0; j < NR; j++) acc[j] += dot_q8sm(wq[j][i], sm[j][i], xc);
+                for (int j = 0; j < NR; j++) {
+                    const float t = dot_q8sm(wq[j][i], sm[j][i], xc);
+                    acc[j] += c < nchunk ? t : 0.f;
                 }
             }
         } else if constexpr (WT == LK_F16) {
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
-                if (c < nchunk) {
-                    const float* xc = x + (size_t)c * 8;
+                const float* xc = XREG ? xr[XREG ? i : 0] : x + (size_t)(c < nchunk ? c : 0u) * 8;
 #pragma unroll
-                    for (int j = 0; j < NR; j++) acc[j] += dot_f16(wq[j][i], xc);
+                for (int j = 0; j < NR; j++) {
+                    const float t = dot_f16(wq[j][i], xc);
+                    acc[j] += c < nchunk ? t : 0.f;
                 }
             }
         } else {  // Q4_K
@@ -423,17 +450,21 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
 #pragma unroll
-                for (int j = 0; j < NR; j++)
-                    hd[j][i] = (c < nchunk && rv[j]) ? *(const uint4*)(ap[j] + 16u * (c >> 3)) : make_uint4(0, 0, 0, 0);
+                for (int j = 0; j < NR; j++) {
+                    const lk_u32x4 hv = *lk_g((const lk_u32x4*)(ap[j] + 16u * ((c < nchunk ? c : 0u) >> 3)));
+                    hd[j][i] = make_uint4(hv.x, hv.y, hv.z, hv.w);
+                }
             }
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
                 const uint32_t c = base + (uint32_t)lane + 64u * i;
-                if (c < nchunk) {
-                    const uint32_t sb = c >> 3, k = c & 7;
-                    const float* xc = x + (size_t)sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
+                const uint32_t cc = c < nchunk ? c : 0u;
+                const uint32_t sb = cc >> 3, k = cc & 7;
+                const float* xc = x + (size_t)sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
 #pragma unroll
-                    for (int j = 0; j < NR; j++) acc[j] += dot_q4k(wq[j][i], hd[j][i], k, xc);
+                for (int j = 0; j < NR; j++) {
+                    const float t = dot_q4k(wq[j][i], hd[j][i], k, xc);
+                    acc[j] += c < nchunk ? t : 0.f;
                 }
             }
         }
@@ -453,8 +484,6 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
             }
         }
     } else if constexpr (MODE == LK_MV_ARGMAX) {
-        __shared__ uint64_t best[4];
-        uint64_t key = 0;
         if (lane == 0) {
 #pragma unroll
             for (int j = 0; j < R; j++) {
@@ -465,13 +494,6 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
                     key = kk > key ? kk : key;
                 }
             }
-            best[threadIdx.x >> 6] = key;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint64_t k = best[0];
-            for (int w = 1; w < 4; w++) k = best[w] > k ? best[w] : k;
-            a.keys[blockIdx.x] = k;
         }
     } else {
         if (lane == 0) {
@@ -485,6 +507,17 @@ __global__ __launch_bounds__(256) void matvec_kernel(const LkMvArgs a) {
                     else s.out[rr[j]] = v;
                 }
             }
+        }
+    }
+    }  // row groups
+    if constexpr (MODE == LK_MV_ARGMAX) {
+        __shared__ uint64_t best[4];
+        if (lane == 0) best[threadIdx.x >> 6] = key;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t k = best[0];
+            for (int w = 1; w < 4; w++) k = best[w] > k ? best[w] : k;
+            a.keys[blockIdx.x] = k;
         }
     }
 }
