@@ -286,3 +286,48 @@ def test_one_kernel_step_past_4096_positions_matches_oracle_on_the_same_cache(n_
     s.close()
     o.close()
     eng.close()
+
+
+def test_two_sessions_stepping_from_two_threads_match_their_solo_runs():
+    """The one-kernel step needs every workgroup resident at once.  Two
+    sessions of one engine decoding from two threads at the same time (each on
+    its own stream) are ordered by the engine's launch gate, so neither
+    step's bounded waits time out, and each thread's greedy ids equal those of
+    the same session run alone."""
+    import threading
+    cfg, tensors, eng, om = build("q8_0", "fused", seed=21)
+    rng = np.random.default_rng(22)
+    prompts = [rng.integers(0, cfg.vocab_size, 16).astype(np.uint32) for _ in range(2)]
+
+    def run(sess, prompt):
+        first = int(np.argmax(sess.prefill(prompt)))
+        return [int(t) for t in sess.decode_greedy(first, len(prompt), 48)]
+
+    solo = []
+    for p in prompts:
+        s = eng.session(128)
+        solo.append(run(s, p))
+        s.close()
+    sessions = [eng.session(128) for _ in prompts]
+    got = [[], []]
+    errors = []
+
+    def worker(i):
+        try:
+            for _ in range(3):
+                got[i].append(run(sessions[i], prompts[i]))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    for i in range(2):
+        assert all(ids == solo[i] for ids in got[i]), i
+    for s in sessions:
+        s.close()
+    eng.close()
