@@ -124,15 +124,32 @@ __device__ __forceinline__ void stage_in(const Ctx& c, const uint64_t* src, uint
     lds_barrier();
 }
 
+// Totals of NB block-wide sums whose per-wave partials sit at red[b*FW + w]:
+// lane 8b + w reads partial (b, w) -- one LDS read for all of them, instead
+// of NB * FW dependent reads -- and the 8 lanes of each row add up by DPP
+// (quad pairs, quad halves, row_ror 4: lane 8b + 4 then holds row b's total).
+static_assert(FW == 8, "the partials of one sum fill 8 adjacent lanes");
+template <int NB>
+__device__ __forceinline__ void block_partials_sum(const float* red, float (&tot)[NB]) {
+    static_assert(NB * FW <= 64, "one lane per partial");
+    const int lane = threadIdx.x & 63;
+    float v = lane < NB * FW ? red[lane] : 0.f;
+    v += lk_dpp<0xB1, 0xF>(v, 0.f);
+    v += lk_dpp<0x4E, 0xF>(v, 0.f);
+    v += lk_dpp<0x124, 0xF>(v, 0.f);
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        tot[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 8 * b + 4));
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = lk_wave_sum(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     lds_barrier();
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < FW; i++) t += red[i];
+    float t[1];
+    block_partials_sum<1>(red, t);
     lds_barrier();
-    return t;
+    return t[0];
 }
 
 // math::rmsnorm (src/math.rs:45-49) of the LDS vector xr into xo (gains g in LDS).
@@ -171,14 +188,10 @@ __device__ __forceinline__ void rmsnorm_rows(const float* xr, const float* g, ui
 #pragma unroll
         for (int b = 0; b < NB; b++) red[b * FW + (threadIdx.x >> 6)] = ss[b];
     lds_barrier();
-    float scale[NB];
+    float tot[NB], scale[NB];
+    block_partials_sum<NB>(red, tot);
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float t = 0.f;
-#pragma unroll
-        for (int i = 0; i < FW; i++) t += red[b * FW + i];
-        scale[b] = 1.0f / sqrtf(t / (float)n + eps);
-    }
+    for (int b = 0; b < NB; b++) scale[b] = 1.0f / sqrtf(tot[b] / (float)n + eps);
 #pragma unroll
     for (int e = 0; e < EPT; e++) {
         const uint32_t i = threadIdx.x + (uint32_t)e * FT;
