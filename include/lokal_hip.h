@@ -269,7 +269,11 @@ int lkhip_embed_gather(const lkhip_weight* table, const uint32_t* ids, size_t n_
  * independent sequences, one query token each.  q: [n_seq][n_heads*head_dim]
  * f32; k_cache/v_cache: f16 [n_seq][n_kv_heads][max_seq][head_dim]; ctx_len
  * (device u32, n_seq) = positions 0..ctx_len-1 are live; out like q.
- * head_dim must be 64; n_heads a multiple of n_kv_heads, group <= 8. */
+ * head_dim must be 64; n_heads a multiple of n_kv_heads, group <= 8.
+ * One launch: chunk partials and the fold in the same kernel, with a scratch
+ * buffer (arrival counters + partials) cached per calling thread and grown on
+ * demand; calls from one thread on different streams share it, so such
+ * calls must not overlap (order them on one stream or synchronise). */
 int lkhip_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* ctx_len,
                       size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq, float* out,
                       void* stream);
