@@ -346,6 +346,22 @@ static int fused_setup(lkhip_engine* e) {
         e->fused_why = "more attention tiles than waves";
         return LKHIP_OK;
     }
+    // the q/k/v rows, attention chunks and merges of an XCD's query heads run
+    // on that XCD's waves (fused.hip)
+    {
+        const uint32_t nh = c.num_attention_heads, G = nh / c.num_key_value_heads;
+        const uint32_t wx = nw / LK_XCDS;
+        bool fits = e->fused_blocks % LK_XCDS == 0;
+        for (uint32_t x = 0; x < LK_XCDS && fits; x++) {
+            const uint32_t h0 = (x * nh + LK_XCDS - 1) / LK_XCDS, h1 = ((x + 1) * nh + LK_XCDS - 1) / LK_XCDS;
+            const uint32_t nq = h1 - h0, nj = nq ? (h1 - 1) / G - h0 / G + 1 : 0;
+            fits = (nq + 2 * nj) * 32 <= wx && nq * LK_FUSED_MAX_CH <= wx;
+        }
+        if (!fits) {
+            e->fused_why = "more q/k/v rows or attention chunks per XCD than its waves";
+            return LKHIP_OK;
+        }
+    }
     // LDS limit for the longest session the one-kernel step serves
     e->fused_lds = lk_fused_lds_bytes(h, I, c.num_attention_heads, c.num_key_value_heads, (uint32_t)e->fused_g,
                                       LK_FUSED_MAX_CH);
@@ -527,9 +543,10 @@ struct lkhip_session {
     hipGraphExec_t exec = nullptr;
     // one-kernel decode step: exchange buffers, epoch counter, error flag
     bool use_fused = false;
+    uint32_t fused_rep = LK_FUSED_REP;  // exchange-vector copies (LKHIP_FUSED_REP)
     uint32_t max_chunks = 0;
     size_t fused_lds = 0;
-    DevBuf xb, qb, pb, ab, xpb, ib, epoch;
+    DevBuf xb, qb, pb, ab, xpb, ib, epoch, xcd_cnt;
     std::unique_ptr<Rows> rows;  // multi-row buffers (prefill, forward_batch), on first use
     DevBuf trace;          // stage timestamps of one block (lkhip_session_set_trace)
     int trace_block = -1;
@@ -639,6 +656,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.st = state;
         a.epoch = s->epoch.as<uint32_t>();
         a.err = s->err.as<uint32_t>();
+        a.xcd_cnt = s->xcd_cnt.as<uint32_t>();
         a.xb = s->xb.as<uint64_t>();
         a.qb = s->qb.as<uint64_t>();
         a.pb = s->pb.as<uint64_t>();
@@ -647,13 +665,15 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.ib = s->ib.as<uint64_t>();
         a.trace = s->trace_block >= 0 ? s->trace.as<uint64_t>() : nullptr;
         a.trace_block = (uint32_t)(s->trace_block >= 0 ? s->trace_block : 0);
+        a.rep = s->fused_rep;
         // The one kernel streams every layer weight of the step: its time is
         // the dequant-matvec time of the layers.
         STEP(lk_fused_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, s->kv_f32,
                              e->fused_blocks, s->fused_lds, st, false),
              C_MATVEC, e->matvec_bytes - e->lm_head->bytes);
         // the last layer's output: f32 halves of the (f32 | epoch) words
-        STEP(enqueue_head(s, (const float*)(s->xb.as<uint64_t>() + (size_t)(c.num_hidden_layers & 1) * h), 2, st),
+        STEP(enqueue_head(s, (const float*)(s->xb.as<uint64_t>() + (size_t)(c.num_hidden_layers & 1) * LK_FUSED_REP * h),
+                          2, st),
              C_LMHEAD, e->lm_head->bytes);
         return hipSuccess;
     }
@@ -793,17 +813,21 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         const size_t h = c.hidden_size, I = c.intermediate_size;
         const size_t qkvd = e->qd + 2 * e->kvd;
         s->max_chunks = (uint32_t)std::min<size_t>((max_seq + 63) / 64, LK_FUSED_MAX_CH);
-        if ((rc = dev_alloc(s->xb, 2 * h * 8)) || (rc = dev_alloc(s->qb, 2 * qkvd * 8)) ||
+        if ((rc = dev_alloc(s->xb, 2 * h * 8 * LK_FUSED_REP)) || (rc = dev_alloc(s->qb, 2 * LK_XCDS * qkvd * 8)) ||
             (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * s->max_chunks * 66 * 8)) ||
-            (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8)) || (rc = dev_alloc(s->xpb, 2 * h * 8)) ||
+            (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8 * LK_FUSED_REP)) ||
+            (rc = dev_alloc(s->xpb, 2 * h * 8 * LK_FUSED_REP)) ||
             (rc = dev_alloc(s->ib, 2 * I * 8)) ||
-            (rc = dev_alloc(s->epoch, 4)))
+            (rc = dev_alloc(s->epoch, 4)) || (rc = dev_alloc(s->xcd_cnt, LK_XCDS * LK_XCD_CNT_STRIDE * 4)))
             return rc;
+        HIP_OR_FAIL(hipMemset(s->xcd_cnt.p, 0, LK_XCDS * LK_XCD_CNT_STRIDE * 4));
         const uint32_t one = 1;
         HIP_OR_FAIL(hipMemcpy(s->epoch.p, &one, 4, hipMemcpyHostToDevice));
         s->fused_lds = lk_fused_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads,
                                           c.num_key_value_heads, (uint32_t)e->fused_g, s->max_chunks);
         s->use_fused = true;
+        const char* rp = getenv("LKHIP_FUSED_REP");
+        if (rp) s->fused_rep = std::min<uint32_t>(LK_FUSED_REP, std::max<uint32_t>(1, (uint32_t)atoi(rp)));
     }
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_state, sizeof(LkStepState), hipHostMallocDefault));
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));

@@ -27,6 +27,8 @@ struct LkFusedArgs {
     LkStepState* st;
     uint32_t* epoch;     // token counter of the exchange epochs
     uint32_t* err;       // set when a bounded wait timed out
+    uint32_t* xcd_cnt;   // fused.hip: per-XCD arrival counters (LK_XCDS words, LK_XCD_CNT_STRIDE apart), zeroed
+                         // once; every launch adds gridDim / LK_XCDS to each
     // exchange buffers of (f32 | epoch) words, two copies by layer parity
     uint64_t* xb;   // [2][h]        layer input x
     uint64_t* qb;   // [2][qd+2kvd]  rotated q, this token's k and v
@@ -40,6 +42,10 @@ struct LkFusedArgs {
     // the block
     uint64_t* trace;
     uint32_t trace_block;
+    // one-kernel step (fused.hip): copies of x, the attention output and x'
+    // published (1..LK_FUSED_REP); each workgroup polls copy blockIdx % rep.
+    // xb, ab and xpb hold [2][LK_FUSED_REP][n] words.
+    uint32_t rep;
     // Batcher rows (fused_rows.hip only): meta = u32 [ids | pos | slots | ...],
     // meta_cap apart; nrows live rows; slot_elems = KV elements between two
     // slots; x_out = the final layer's f32 rows [nrows][h]
@@ -66,6 +72,13 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_MAX_CH 64u
 // Longest session of the multi-row one-kernel step (one tile per wave).
 #define LK_FUSED_ROWS_MAX_SEQ 4096u
+// Exchange-vector copies the single-row step's buffers are laid out for.
+#define LK_FUSED_REP 8u
+// XCDs of the part (workgroup b runs on XCD b % LK_XCDS) and the hardware
+// register holding a wave's XCD id (s_getreg_b32 HW_REG_XCC_ID, bits 3:0).
+#define LK_XCDS 8u
+#define LK_XCD_CNT_STRIDE 64u
+#define LK_HWREG_XCC_ID (20 | (0 << 6) | ((4 - 1) << 11))
 // Waves per workgroup.
 #define LK_FUSED_WAVES 8u
 

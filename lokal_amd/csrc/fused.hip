@@ -66,6 +66,31 @@ namespace lkf {
 
 using namespace lk;
 
+// XCD-local exchange words: plain stores land in the XCD's L2, nontemporal
+// loads bypass the CU's L1 and read that L2.  Valid only between workgroups
+// of one XCD.
+__device__ __forceinline__ void publish_x(uint64_t* p, float v, uint32_t ep) {
+    *(__attribute__((address_space(1))) uint64_t*)p = word(v, ep);
+}
+__device__ __forceinline__ uint64_t ld_x(const uint64_t* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint64_t*)p);
+}
+__device__ __forceinline__ float await_x(const Ctx& c, const uint64_t* p, uint32_t ep) {
+    uint64_t w = ld_x(p);
+    for (uint32_t n = 0; (uint32_t)(w >> 32) != ep; n++) {
+        __builtin_amdgcn_s_sleep(1);
+        w = ld_x(p);
+        if ((n & 255) == 255) {
+            if (__hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+            if (n > (1u << 21)) {
+                __hip_atomic_store(c.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    return __uint_as_float((uint32_t)w);
+}
+
 template <int WT, int NCHH, int NCHI, typename KV, int G>
 __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) {
     extern __shared__ float lds[];
@@ -91,6 +116,17 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // flight (vector loads retire in order) -- a full HBM round trip per
     // row issue.  LDS reads wait on their own counter.
     LkFusedLayer* lay = (LkFusedLayer*)(wv + FW * 256);
+    uint32_t* slot_lds = (uint32_t*)(lay + LK_FUSED_MAX_LAYERS);
+    // This workgroup's XCD (hardware id) and its slot among the XCD's
+    // gridDim / LK_XCDS workgroups: the CP hands workgroups to the XCDs in
+    // turn, so each XCD holds the same number of them, and an arrival counter
+    // per XCD numbers them (counters only grow: slot = count mod the XCD's
+    // share).
+    const uint32_t xcd = __builtin_amdgcn_s_getreg(LK_HWREG_XCC_ID) & (LK_XCDS - 1);
+    const uint32_t nslot = gridDim.x / LK_XCDS;
+    if (threadIdx.x == 0)
+        *slot_lds = __hip_atomic_fetch_add(a.xcd_cnt + xcd * LK_XCD_CNT_STRIDE, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) % nslot;
     {
         const uint32_t* src = (const uint32_t*)a.layers;
         uint32_t* dst = (uint32_t*)lay;
@@ -115,17 +151,37 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     const uint32_t nch = (ntile + tpw - 1) / tpw;  // partials per head
     const uint32_t nps = a.max_chunks;             // partial slots per head
 
+    // XCD-local work.  Query head hq belongs to XCD hq * 8 / nh, so XCD x
+    // owns heads [h0, h1) and the kv heads [j0, j1] they read.  The q/k/v rows
+    // of those heads (S1), their attention chunks (S2) and merges (S3) run on
+    // XCD x's workgroups, and the words these three stages exchange stay in
+    // its L2: plain stores, nontemporal (L1-bypassing) loads -- a hop inside
+    // an XCD costs ~0.28 us against ~0.6 us through the memory-side cache.
+    // Each XCD computes the k/v rows of its kv heads itself; the XCD owning a
+    // kv head's first query head writes them to the cache.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's LDS store
+    __builtin_amdgcn_s_barrier();
+    const uint32_t lw = (uint32_t)wave * nslot + __builtin_amdgcn_readfirstlane(*slot_lds);  // XCD-local wave index
+    const uint32_t h0 = (xcd * nh + LK_XCDS - 1) / LK_XCDS, h1 = ((xcd + 1) * nh + LK_XCDS - 1) / LK_XCDS;
+    const uint32_t nq = h1 - h0;
+    const uint32_t j0 = nq ? h0 / G : 0, nj = nq ? (h1 - 1) / G - j0 + 1 : 0;
     // S1 work of this wave: q/k/v rows (i, i+32) of one head
-    const uint32_t U1 = (nh + 2 * nkv) * 32;
-    const bool has1 = c.gw < (int)U1;
+    const uint32_t U1 = (nq + 2 * nj) * 32;
+    const bool has1 = lw < U1;
     uint32_t kind = 0, head = 0, ip = 0;
+    bool kv_writer = false;
     if (has1) {
-        const uint32_t hh = (uint32_t)c.gw / 32;
-        ip = (uint32_t)c.gw % 32;
-        if (hh < nh) { kind = 0; head = hh; }
-        else if (hh < nh + nkv) { kind = 1; head = hh - nh; }
-        else { kind = 2; head = hh - nh - nkv; }
+        ip = lw % 32;
+        const uint32_t it = lw / 32;
+        if (it < nq) { kind = 0; head = h0 + it; }
+        else {
+            const uint32_t jt = it - nq;
+            kind = 1 + (jt & 1);
+            head = j0 + jt / 2;
+            kv_writer = (head * G) * LK_XCDS / nh == xcd;
+        }
     }
+    uint64_t* QX = a.qb + (size_t)xcd * qkvd;  // this XCD's q/k/v words (parity copies LK_XCDS * qkvd apart)
     const bool tracing = a.trace != nullptr;  // every workgroup records its own row
     if (tracing && threadIdx.x == 0)
         for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) ltr[k] = 0;
@@ -184,10 +240,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         const LkFusedLayer& ly = lay[L];
         const uint32_t ep = base * (nL + 1) + L + 1;
         const uint32_t par = L & 1;
-        uint64_t* QB = a.qb + (size_t)par * qkvd;
+        uint64_t* QB = QX + (size_t)par * LK_XCDS * qkvd;
         uint64_t* PB = a.pb + (size_t)par * nh * nps * 66;  // [head][chunk][m, l, acc[64]]
-        uint64_t* AB = a.ab + (size_t)par * qd;
-        uint64_t* XP = a.xpb + (size_t)par * h;
+        // x, the attention output and x' are published in `rep` copies (one
+        // per XCD at rep = 8: a vector polled by every workgroup is then read
+        // from 8 places instead of one); a workgroup polls copy blockIdx % rep
+        const uint32_t rep = a.rep, cp = blockIdx.x % rep;
+        uint64_t* AB = a.ab + (size_t)par * LK_FUSED_REP * qd;
+        uint64_t* XP = a.xpb + (size_t)par * LK_FUSED_REP * h;
         uint64_t* IB = a.ib + (size_t)par * I;
         // Weight rows are issued one or two stages before they are used, after
         // the stage's own outputs are published: vector loads retire in issue
@@ -219,7 +279,43 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 b2 = lk_g(bias)[head * 64 + ip + 32];
             }
         }
-        if (L > 0) stage_in<8>(c, a.xb + (size_t)par * h, h, ep, xres, 1);
+        // ---- this wave's attention item (S2)
+        const bool has2 = lw < nq * nch;  // this wave has an attention item on its XCD
+        const uint32_t hq = h0 + lw / nch, ck = lw % nch;
+        const uint32_t j = hq / G;
+        const uint32_t t0 = ck * tpw, t1 = t0 + tpw < ntile ? t0 + tpw : ntile;
+        const bool chunk_cur = t1 == ntile;  // the chunk holding position pos
+        const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+        const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+        const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
+        // Cached positions (< pos) do not depend on this token: the first
+        // tile is loaded before the wait for q.  The cache holds whole
+        // 64-position tiles (its per-head stride is max_seq rounded up to
+        // 64), so every row of a tile is in bounds; rows >= pos are
+        // replaced (pos) or masked (> pos) below.
+        uint4 kraw[KC], vraw[KC];
+        // K rows from pos on are this token's (in flight from S1) or
+        // unwritten: read row pos - 1 instead (the lane's score is
+        // replaced or masked below)
+        auto load_k = [&](uint32_t t) {
+            uint32_t krow = t * 64u + (uint32_t)lane;
+            krow = krow < pos ? krow : (pos ? pos - 1 : 0);
+            const KV* Kl = K + krow * 64u;
+#pragma unroll
+            for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
+        };
+        auto load_v = [&](uint32_t t) {
+            const KV* Vl = V + (t * 64u + sub) * 64u + dq;
+#pragma unroll
+            for (int q = 0; q < KC; q++)
+                vraw[q] = *(const uint4*)(Vl + (KV32 ? (q / 2) * 8 * 64 + (q & 1) * 4 : q * 8 * 64));
+        };
+        // f16: a tile's K and V fit in registers together; f32: V follows the scores
+        auto load_tile = [&](uint32_t t) {
+            load_k(t);
+            if constexpr (!KV32) load_v(t);
+        };
+        if (L > 0) stage_in<8>(c, a.xb + ((size_t)par * LK_FUSED_REP + cp) * h, h, ep, xres, 1);
         LKF_SUB(15);
         rmsnorm_lds(xres, gin, h, a.eps, xin, red);
         LKF_SUB(16);
@@ -233,16 +329,18 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 d2 += b2;
                 if (kind < 2) rot(d1, d2, rc, rsn);
                 if (kind == 0) {
-                    publish(QB + r, d1, ep);
-                    publish(QB + r + 32, d2, ep);
+                    publish_x(QB + r, d1, ep);
+                    publish_x(QB + r + 32, d2, ep);
                 } else {
-                    KV* cache = (KV*)(kind == 1 ? a.kc : a.vc) + (size_t)L * a.kv_layer +
-                                ((size_t)head * a.max_seq + pos) * 64;
-                    kv_put(cache + ip, d1);
-                    kv_put(cache + ip + 32, d2);
+                    if (kv_writer) {
+                        KV* cache = (KV*)(kind == 1 ? a.kc : a.vc) + (size_t)L * a.kv_layer +
+                                    ((size_t)head * a.max_seq + pos) * 64;
+                        kv_put(cache + ip, d1);
+                        kv_put(cache + ip + 32, d2);
+                    }
                     const uint32_t off = qd + (kind == 2 ? kvd : 0) + r;
-                    publish(QB + off, kv_round(d1, KV32), ep);
-                    publish(QB + off + 32, kv_round(d2, KV32), ep);
+                    publish_x(QB + off, kv_round(d1, KV32), ep);
+                    publish_x(QB + off + 32, kv_round(d2, KV32), ep);
                 }
             }
         }
@@ -263,7 +361,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
             }
         };
-        if (c.gw >= (int)(nh * nch)) issue_ahead();
+        if (!has2) issue_ahead();
         LKF_MARK(2 + 6 * L + 0);
         // ---------------- S2: attention partials.  Item = (query head, chunk
         // of tpw tiles of 64 positions), one wave each, spread over the grid
@@ -272,42 +370,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // position), folds the tile's max and sum into its running softmax,
         // and accumulates P.V with lane = (position group lane & 7, dims
         // 8 * (lane >> 3) ..+7).
-        if (c.gw < (int)(nh * nch)) {
-            const uint32_t hq = (uint32_t)c.gw / nch, ck = (uint32_t)c.gw % nch;
-            const uint32_t j = hq / G;
-            const uint32_t t0 = ck * tpw, t1 = t0 + tpw < ntile ? t0 + tpw : ntile;
-            const bool chunk_cur = t1 == ntile;  // the chunk holding position pos
+        if (has2) {
             LKF_SUB(0);
-            const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
-            const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
-            const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
-            // Cached positions (< pos) do not depend on this token: the first
-            // tile is loaded before the wait for q.  The cache holds whole
-            // 64-position tiles (its per-head stride is max_seq rounded up to
-            // 64), so every row of a tile is in bounds; rows >= pos are
-            // replaced (pos) or masked (> pos) below.
-            uint4 kraw[KC], vraw[KC];
-            // K rows from pos on are this token's (in flight from S1) or
-            // unwritten: read row pos - 1 instead (the lane's score is
-            // replaced or masked below)
-            auto load_k = [&](uint32_t t) {
-                uint32_t krow = t * 64u + (uint32_t)lane;
-                krow = krow < pos ? krow : (pos ? pos - 1 : 0);
-                const KV* Kl = K + krow * 64u;
-#pragma unroll
-                for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
-            };
-            auto load_v = [&](uint32_t t) {
-                const KV* Vl = V + (t * 64u + sub) * 64u + dq;
-#pragma unroll
-                for (int q = 0; q < KC; q++)
-                    vraw[q] = *(const uint4*)(Vl + (KV32 ? (q / 2) * 8 * 64 + (q & 1) * 4 : q * 8 * 64));
-            };
-            // f16: a tile's K and V fit in registers together; f32: V follows the scores
-            auto load_tile = [&](uint32_t t) {
-                load_k(t);
-                if constexpr (!KV32) load_v(t);
-            };
             load_tile(t0);
             issue_ahead();
             LKF_SUB(1);
@@ -315,13 +379,13 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 const uint64_t* sq = QB + hq * 64 + lane;
                 const uint64_t* sk = QB + qd + j * 64 + lane;
                 const uint64_t* sv = QB + qd + kvd + j * 64 + lane;
-                const uint64_t w0 = ld_word(sq);
-                const uint64_t w1 = chunk_cur ? ld_word(sk) : 0;
-                const uint64_t w2 = chunk_cur ? ld_word(sv) : 0;
-                wq[lane] = (uint32_t)(w0 >> 32) == ep ? __uint_as_float((uint32_t)w0) : await(c, sq, ep);
+                const uint64_t w0 = ld_x(sq);
+                const uint64_t w1 = chunk_cur ? ld_x(sk) : 0;
+                const uint64_t w2 = chunk_cur ? ld_x(sv) : 0;
+                wq[lane] = (uint32_t)(w0 >> 32) == ep ? __uint_as_float((uint32_t)w0) : await_x(c, sq, ep);
                 if (chunk_cur) {
-                    wk[lane] = (uint32_t)(w1 >> 32) == ep ? __uint_as_float((uint32_t)w1) : await(c, sk, ep);
-                    wvc[lane] = (uint32_t)(w2 >> 32) == ep ? __uint_as_float((uint32_t)w2) : await(c, sv, ep);
+                    wk[lane] = (uint32_t)(w1 >> 32) == ep ? __uint_as_float((uint32_t)w1) : await_x(c, sk, ep);
+                    wvc[lane] = (uint32_t)(w2 >> 32) == ep ? __uint_as_float((uint32_t)w2) : await_x(c, sv, ep);
                 }
             }
             wave_sync_lds();
@@ -423,19 +487,19 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             }
             uint64_t* out = PB + ((size_t)hq * nps + ck) * 66;
             if (lane == 0) {
-                publish(out, m, ep);
-                publish(out + 1, l, ep);
+                publish_x(out, m, ep);
+                publish_x(out + 1, l, ep);
             }
             if ((lane & 7) == 4) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) publish(out + 2 + dq + e, acc[e], ep);
+                for (int e = 0; e < 8; e++) publish_x(out + 2 + dq + e, acc[e], ep);
             }
             LKF_SUB(6);
         }
         LKF_MARK(2 + 6 * L + 1);
         // ---------------- S3: merge each head's chunks -> attention output (lane = dim)
-        if (c.gw < (int)nh) {
-            const uint32_t hq = (uint32_t)c.gw;
+        if (lw < nq) {
+            const uint32_t hq = h0 + lw;
             const uint64_t* pp = PB + (size_t)hq * nps * 66;
             // lane k < nch fetches tile k's (m, l); every lane fetches its dim
             // of every tile's acc, 16 tiles' words in flight at a time, and
@@ -443,12 +507,12 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             const bool mk = lane < (int)nch;
             const uint64_t* pm = pp + (mk ? lane : 0) * 66;
             const uint64_t epw = (uint64_t)ep << 32;
-            uint64_t wmw = mk ? ld_word(pm) : epw, wlw = mk ? ld_word(pm + 1) : epw;
+            uint64_t wmw = mk ? ld_x(pm) : epw, wlw = mk ? ld_x(pm + 1) : epw;
             float mv = -INFINITY, lv = 0.f, M = 0.f, sc = 0.f, Ls = 0.f, A = 0.f;
             for (uint32_t k0 = 0; k0 < nch; k0 += 16) {
                 uint64_t wa[16];
 #pragma unroll
-                for (int k = 0; k < 16; k++) wa[k] = k0 + k < nch ? ld_word(pp + (k0 + k) * 66 + 2 + lane) : epw;
+                for (int k = 0; k < 16; k++) wa[k] = k0 + k < nch ? ld_x(pp + (k0 + k) * 66 + 2 + lane) : epw;
                 for (uint32_t r = 0;; r++) {
                     bool done = (uint32_t)(wmw >> 32) == ep && (uint32_t)(wlw >> 32) == ep;
 #pragma unroll
@@ -462,11 +526,11 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                         }
                     }
                     __builtin_amdgcn_s_sleep(1);
-                    if ((uint32_t)(wmw >> 32) != ep) wmw = ld_word(pm);
-                    if ((uint32_t)(wlw >> 32) != ep) wlw = ld_word(pm + 1);
+                    if ((uint32_t)(wmw >> 32) != ep) wmw = ld_x(pm);
+                    if ((uint32_t)(wlw >> 32) != ep) wlw = ld_x(pm + 1);
 #pragma unroll
                     for (int k = 0; k < 16; k++)
-                        if ((uint32_t)(wa[k] >> 32) != ep) wa[k] = ld_word(pp + (k0 + k) * 66 + 2 + lane);
+                        if ((uint32_t)(wa[k] >> 32) != ep) wa[k] = ld_x(pp + (k0 + k) * 66 + 2 + lane);
                 }
                 if (k0 == 0) LKF_SUB(20);
                 if (k0 == 0) {
@@ -488,17 +552,17 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 }
             }
             LKF_SUB(21);
-            publish(AB + hq * 64 + lane, A / Ls, ep);
+            for (uint32_t k = 0; k < rep; k++) publish(AB + (size_t)k * qd + hq * 64 + lane, A / Ls, ep);
         }
         LKF_MARK(2 + 6 * L + 2);
         // ---------------- S4: o_proj + residual -> x'
         {
             const int u = c.gw;
-            stage_in<4>(c, AB, qd, ep, xin, -1);
+            stage_in<4>(c, AB + (size_t)cp * qd, qd, ep, xin, -1);
             LKF_SUB(12);
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
-                if (lane == 0) publish(XP + u, xres[u] + d, ep);
+                if (lane < (int)rep) publish(XP + (size_t)lane * h + u, xres[u] + d, ep);
             }
             LKF_SUB(13);
             // the next stage's rows: issued after the publish, because a wave
@@ -518,7 +582,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         LKF_MARK(2 + 6 * L + 3);
         // ---------------- S5: RMSNorm + gate/up + SwiGLU -> inner
         {
-            stage_in<8>(c, XP, h, ep, xres, 1);
+            stage_in<8>(c, XP + (size_t)cp * h, h, ep, xres, 1);
             LKF_SUB(8);
             rmsnorm_lds(xres, gpost, h, a.eps, xin, red);
             LKF_SUB(9);
@@ -563,19 +627,19 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // ---------------- S6: down + residual -> x of layer L+1
         {
             const uint32_t epn = ep + 1;
-            uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * h;
+            uint64_t* XN = a.xb + (size_t)((L + 1) & 1) * LK_FUSED_REP * h;
             stage_in<24>(c, IB, I, ep, xin, 1);
             LKF_SUB(7);
             if (c.gw < (int)h) {
                 const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
                 LKF_SUB(19);
-                if (lane == 0) publish(XN + c.gw, xres[c.gw] + d, epn);
+                if (lane < (int)rep) publish(XN + (size_t)lane * h + c.gw, xres[c.gw] + d, epn);
             }
             for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
                 Row<WT, NCHI> rr;
                 row_issue(rr, ly.down, (uint32_t)uu, lane);
                 const float d = lk_wave_sum(row_dot(rr, xin, I, lane));
-                if (lane == 0) publish(XN + uu, xres[uu] + d, epn);
+                if (lane < (int)rep) publish(XN + (size_t)lane * h + uu, xres[uu] + d, epn);
             }
             if (L + 1 < nL) {  // read after the next stage_in's barrier
                 gains_issue(lay[L + 1]);
@@ -602,7 +666,7 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
     uint32_t vmax = I > h ? I : h;
     if (nh * 64 > vmax) vmax = nh * 64;
     return ((size_t)vmax + h + 16 + 2 * (size_t)h + (h & 1) + 2 * LKF_TRACE_MAX + (size_t)FW * 256) * 4 +
-           LK_FUSED_MAX_LAYERS * sizeof(LkFusedLayer);
+           LK_FUSED_MAX_LAYERS * sizeof(LkFusedLayer) + 16;
 }
 int lk_fused_threads() { return FT; }
 
