@@ -317,11 +317,15 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         };
         if (L > 0) stage_in<8>(c, a.xb + ((size_t)par * LK_FUSED_REP + cp) * h, h, ep, xres, 1);
         LKF_SUB(15);
-        rmsnorm_lds(xres, gin, h, a.eps, xin, red);
         LKF_SUB(16);
         if (has1) {
-            float d1 = lk_wave_sum(row_dot(q1, xin, h, lane));
-            float d2 = lk_wave_sum(row_dot(q2, xin, h, lane));
+            // RMSNorm of the lane's slice of x (per wave, no block barrier) and
+            // both rows' dots, their wave sums interleaved
+            float xr[NCHH][ChunkTraits<WT>::elems];
+            norm_slice<WT, NCHH>(xres, gin, h, a.eps, lane, xr);
+            float dd[2] = {row_dot_reg(q1, xr, h, lane), row_dot_reg(q2, xr, h, lane)};
+            wave_sums(dd);
+            float d1 = dd[0], d2 = dd[1];
             LKF_SUB(17);
             if (lane == 0) {
                 const uint32_t r = head * 64 + ip;
@@ -584,15 +588,24 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         {
             stage_in<8>(c, XP + (size_t)cp * h, h, ep, xres, 1);
             LKF_SUB(8);
-            rmsnorm_lds(xres, gpost, h, a.eps, xin, red);
+            // RMSNorm of the lane's slice of x' by every wave (no block
+            // barrier), reused by all of the wave's gate/up rows
+            float xr[NCHH][ChunkTraits<WT>::elems];
+            norm_slice<WT, NCHH>(xres, gpost, h, a.eps, lane, xr);
             LKF_SUB(9);
+            {
+                float dd[2 * LKF_KB];
 #pragma unroll
-            for (int k = 0; k < LKF_KB; k++) {
-                const int uu = unit_of(k);
-                if (k < nunits && uu < (int)U5) {
-                    const float gg = lk_wave_sum(row_dot(gq[k], xin, h, lane));
-                    const float up = lk_wave_sum(row_dot(uq[k], xin, h, lane));
-                    if (lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
+                for (int k = 0; k < LKF_KB; k++) {
+                    dd[2 * k] = row_dot_reg(gq[k], xr, h, lane);
+                    dd[2 * k + 1] = row_dot_reg(uq[k], xr, h, lane);
+                }
+                wave_sums(dd);
+#pragma unroll
+                for (int k = 0; k < LKF_KB; k++) {
+                    const int uu = unit_of(k);
+                    const float gg = dd[2 * k], up = dd[2 * k + 1];
+                    if (k < nunits && uu < (int)U5 && lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
                 }
             }
             LKF_SUB(10);
@@ -610,14 +623,18 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                         row_issue(pr[x], ly.up, (uint32_t)ux, lane);
                     }
                 }
+                float dd[2 * XU];
+#pragma unroll
+                for (int x = 0; x < XU; x++) {
+                    dd[2 * x] = row_dot_reg(gr[x], xr, h, lane);
+                    dd[2 * x + 1] = row_dot_reg(pr[x], xr, h, lane);
+                }
+                wave_sums(dd);
 #pragma unroll
                 for (int x = 0; x < XU; x++) {
                     const int ux = uu + x * c.nw;
-                    if (ux < (int)U5) {
-                        const float gg = lk_wave_sum(row_dot(gr[x], xin, h, lane));
-                        const float up = lk_wave_sum(row_dot(pr[x], xin, h, lane));
-                        if (lane == 0) publish(IB + ux, gg / (1.0f + expf(-gg)) * up, ep);
-                    }
+                    const float gg = dd[2 * x], up = dd[2 * x + 1];
+                    if (ux < (int)U5 && lane == 0) publish(IB + ux, gg / (1.0f + expf(-gg)) * up, ep);
                 }
             }
             if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);

@@ -261,6 +261,89 @@ __device__ __forceinline__ void unpack8(const U4 (&raw)[N], int q, bool f32, flo
     }
 }
 
+// N wave sums at once: each DPP step is applied to all N values before the
+// next, so the N dependent chains overlap (lk_wave_sum's order of additions:
+// each result is bit-identical to it).
+template <int N>
+__device__ __forceinline__ void wave_sums(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0xB1, 0xF>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0x4E, 0xF>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0x124, 0xF>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0x128, 0xF>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0x142, 0xA>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += lk_dpp<0x143, 0xC>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
+}
+
+// This lane's slice of an LDS vector for rows of NCH 16-byte chunks (lane l
+// takes chunks l + 64 i), read once and reused by every row: chunk
+// elements are contiguous (Q8_0, F16, Q8_SM); Q4_K's 16 low-nibble then 16
+// high-nibble elements of its chunk (sub-block pair k >> 1, half k & 1 of
+// super-block ch >> 3).
+template <int WT, int NCH>
+__device__ __forceinline__ void x_slice(const float* x, uint32_t cols, int lane,
+                                        float (&xr)[NCH][ChunkTraits<WT>::elems]) {
+    constexpr uint32_t CE = ChunkTraits<WT>::elems;
+    const uint32_t nchunk = cols / CE;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t ch0 = (uint32_t)lane + 64u * i;
+        const uint32_t ch = ch0 < nchunk ? ch0 : 0u;
+        if constexpr (WT == LK_Q4_K) {
+            const uint32_t sb = ch >> 3, k = ch & 7;
+            const float* xl = x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16;
+#pragma unroll
+            for (uint32_t e = 0; e < 16; e += 4) {
+                const float4 lo = *(const float4*)(xl + e), hi = *(const float4*)(xl + 32 + e);
+                xr[i][e] = lo.x; xr[i][e + 1] = lo.y; xr[i][e + 2] = lo.z; xr[i][e + 3] = lo.w;
+                xr[i][16 + e] = hi.x; xr[i][16 + e + 1] = hi.y; xr[i][16 + e + 2] = hi.z; xr[i][16 + e + 3] = hi.w;
+            }
+        } else {
+            const float* xc = x + (size_t)ch * CE;
+#pragma unroll
+            for (uint32_t e = 0; e < CE; e += 4) {
+                const float4 v = *(const float4*)(xc + e);
+                xr[i][e] = v.x; xr[i][e + 1] = v.y; xr[i][e + 2] = v.z; xr[i][e + 3] = v.w;
+            }
+        }
+    }
+}
+
+// math::rmsnorm (src/math.rs:45-49) of an LDS vector, by each wave for its
+// own lanes' slice: the sum of squares over the wave (no block barrier),
+// then (x * scale) * g per element, both products rounded as the CPU path
+// rounds them.
+template <int WT, int NCH>
+__device__ __forceinline__ void norm_slice(const float* x, const float* g, uint32_t n, float eps, int lane,
+                                           float (&xr)[NCH][ChunkTraits<WT>::elems]) {
+    constexpr uint32_t CE = ChunkTraits<WT>::elems;
+    const uint32_t nchunk = n / CE;
+    x_slice<WT, NCH>(x, n, lane, xr);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const bool ok = (uint32_t)lane + 64u * i < nchunk;
+#pragma unroll
+        for (uint32_t e = 0; e < CE; e++) ss = ok ? fmaf(xr[i][e], xr[i][e], ss) : ss;
+    }
+    ss = lk_wave_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    float gr[NCH][CE];
+    x_slice<WT, NCH>(g, n, lane, gr);
+#pragma unroll
+    for (int i = 0; i < NCH; i++)
+#pragma unroll
+        for (uint32_t e = 0; e < CE; e++) xr[i][e] = __fmul_rn(__fmul_rn(xr[i][e], scale), gr[i][e]);
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
