@@ -361,6 +361,22 @@ static int fused_setup(lkhip_engine* e) {
             e->fused_why = "more q/k/v rows or attention chunks per XCD than its waves";
             return LKHIP_OK;
         }
+        // the step's workgroups must land evenly on XCDs 0..LK_XCDS-1 (it
+        // numbers them per XCD by the hardware id)
+        DevBuf ids;
+        int rc = dev_alloc(ids, (size_t)e->fused_blocks * 4);
+        if (rc) return rc;
+        HIP_OR_FAIL(lk_xcd_probe_launch(ids.as<uint32_t>(), e->fused_blocks, nullptr));
+        std::vector<uint32_t> h_ids(e->fused_blocks);
+        HIP_OR_FAIL(hipMemcpy(h_ids.data(), ids.p, h_ids.size() * 4, hipMemcpyDeviceToHost));
+        uint32_t per[16] = {};
+        for (uint32_t id : h_ids) per[id & 15]++;
+        for (uint32_t x = 0; x < 16; x++)
+            if (per[x] != (x < LK_XCDS ? e->fused_blocks / LK_XCDS : 0)) fits = false;
+        if (!fits) {
+            e->fused_why = "the device does not spread a launch's workgroups evenly over 8 XCDs";
+            return LKHIP_OK;
+        }
     }
     // LDS limit for the longest session the one-kernel step serves
     e->fused_lds = lk_fused_lds_bytes(h, I, c.num_attention_heads, c.num_key_value_heads, (uint32_t)e->fused_g,

@@ -83,6 +83,8 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_WAVES 8u
 
 int lk_fused_threads();
+// Writes the XCD id (0..15) of each workgroup of a `blocks`-workgroup launch.
+hipError_t lk_xcd_probe_launch(uint32_t* out, unsigned blocks, hipStream_t st);
 // The multi-row one-kernel step (fused_rows.hip): 4 or LK_FUSED_ROWS Batcher
 // rows per launch (fewer are padded), f16 KV.
 #define LK_FUSED_ROWS 8u

@@ -687,6 +687,16 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 }
 int lk_fused_threads() { return FT; }
 
+// The XCD id of every workgroup of a `blocks`-workgroup launch (one thread
+// each), for the host to check the placement the one-kernel step relies on.
+__global__ void xcd_probe_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = __builtin_amdgcn_s_getreg(LK_HWREG_XCC_ID) & 15u;
+}
+hipError_t lk_xcd_probe_launch(uint32_t* out, unsigned blocks, hipStream_t st) {
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(blocks), dim3(64), 0, st, out);
+    return hipGetLastError();
+}
+
 template <int WT, int NCHH, int NCHI, typename KV, int G>
 static hipError_t launch_t(const LkFusedArgs& a, unsigned blocks, size_t lds, hipStream_t st, bool setup) {
     auto kfn = lkf::fused_step_kernel<WT, NCHH, NCHI, KV, G>;
