@@ -439,9 +439,9 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                 if (k < nunits && uu < (int)I) {
 #pragma unroll 1
                     for (int b = 0; b < NB; b++) {
-                        const float gg = lk_wave_sum(row_dot(gq[k], xin + b * h, h, lane));
-                        const float up = lk_wave_sum(row_dot(uq[k], xin + b * h, h, lane));
-                        if (lane == 0) publish(IB + (size_t)b * I + uu, gg / (1.0f + expf(-gg)) * up, ep);
+                        float gu[2] = {row_dot(gq[k], xin + b * h, h, lane), row_dot(uq[k], xin + b * h, h, lane)};
+                        wave_sums(gu);  // the two sums interleaved
+                        if (lane == 0) publish(IB + (size_t)b * I + uu, gu[0] / (1.0f + expf(-gu[0])) * gu[1], ep);
                     }
                 }
             }
@@ -451,9 +451,9 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                 row_issue(pr, ly.up, (uint32_t)uu, lane);
 #pragma unroll 1
                 for (int b = 0; b < NB; b++) {
-                    const float gg = lk_wave_sum(row_dot(gr, xin + b * h, h, lane));
-                    const float up = lk_wave_sum(row_dot(pr, xin + b * h, h, lane));
-                    if (lane == 0) publish(IB + (size_t)b * I + uu, gg / (1.0f + expf(-gg)) * up, ep);
+                    float gu[2] = {row_dot(gr, xin + b * h, h, lane), row_dot(pr, xin + b * h, h, lane)};
+                    wave_sums(gu);
+                    if (lane == 0) publish(IB + (size_t)b * I + uu, gu[0] / (1.0f + expf(-gu[0])) * gu[1], ep);
                 }
             }
             if (c.gw < (int)h) row_issue(dn, ly.down, (uint32_t)c.gw, lane);
