@@ -215,7 +215,7 @@ __device__ __forceinline__ size_t row_aux_bytes(uint32_t cols) {
 template <int WT, int NCH>
 struct Row {
     uint4 q[NCH];
-    uint4 hd[NCH];  // Q4_K super-block heads
+    uint32_t hd[NCH];  // Q4_K: dword (lane & 3) of the chunk's 16-byte super-block head (see q4k_head)
     uint32_t d[NCH];  // Q8_0 block scales, raw f16 bits: converted at use, so issuing never waits
     uint2 sm[NCH];    // Q8_SM (s, m) bits
 };
@@ -245,11 +245,21 @@ __device__ __forceinline__ void row_issue(Row<WT, NCH>& R, const LkDevW& w, uint
         R.q[i] = ld_stream16(rp + 16u * ch);
         if constexpr (WT == LK_Q8_0) R.d[i] = (uint32_t)lk_g((const uint16_t*)ap)[ch >> 1];
         if constexpr (WT == LK_Q8_SM) R.sm[i] = ld_sm(ap, ch);
-        if constexpr (WT == LK_Q4_K) {
-            const lk_u32x4 hv = *lk_g((const lk_u32x4*)(ap + 16u * (ch >> 3)));
-            R.hd[i] = make_uint4(hv.x, hv.y, hv.z, hv.w);
-        }
+        if constexpr (WT == LK_Q4_K) R.hd[i] = lk_g((const uint32_t*)(ap + 16u * (ch >> 3)))[lane & 3];
     }
+}
+
+// A Q4_K chunk's super-block head from the dwords its quad of lanes holds:
+// lanes 8m..8m+7 share one head (8 chunks of 32 values per super-block, and
+// a row's chunk count is a multiple of 8), and lane l holds its dword l & 3,
+// so each lane rebuilds the whole head by 4 quad-broadcast moves -- 1 VGPR
+// per held chunk instead of 4.  Every lane of the wave must execute this.
+__device__ __forceinline__ uint4 q4k_head(uint32_t w) {
+    const int v = (int)w;
+    return make_uint4((uint32_t)__builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, true),
+                      (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, true),
+                      (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, true),
+                      (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, true));
 }
 
 // This lane's partial dot of the row with x (LDS); reduce across the wave after.
@@ -274,7 +284,7 @@ __device__ __forceinline__ float row_dot(const Row<WT, NCH>& R, const float* x, 
             t = dot_q8sm(R.q[i], R.sm[i], x + ch * 16);
         } else {
             const uint32_t sb = ch >> 3, k = ch & 7;
-            t = dot_q4k(R.q[i], R.hd[i], k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
+            t = dot_q4k(R.q[i], q4k_head(R.hd[i]), k, x + sb * 256 + (k >> 1) * 64 + (k & 1) * 16);
         }
         acc += ok ? t : 0.f;
     }
@@ -307,7 +317,7 @@ __device__ __forceinline__ float row_dot_reg(const Row<WT, NCH>& R, const float 
                 xx[e] = xr[i][e];
                 xx[32 + e] = xr[i][16 + e];
             }
-            t = dot_q4k(R.q[i], R.hd[i], ch & 7, xx);
+            t = dot_q4k(R.q[i], q4k_head(R.hd[i]), ch & 7, xx);
         }
         acc += ch < nchunk ? t : 0.f;
     }
