@@ -78,15 +78,29 @@ __global__ __launch_bounds__(HT) void lm_head_kernel(const LkHeadArgs a) {
         Row<WT, NCH> rr[R];
 #pragma unroll
         for (int k = 0; k < R; k++) row_issue(rr[k], a.w, r0 + k < V ? r0 + k : V - 1, lane);
+        // the R rows' dots, their wave sums interleaved (each result equals lk_wave_sum's)
+        float d[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] = row_dot_reg(rr[k], xr, h, lane);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0xB1, 0xF>(d[k], 0.f);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0x4E, 0xF>(d[k], 0.f);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0x124, 0xF>(d[k], 0.f);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0x128, 0xF>(d[k], 0.f);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0x142, 0xA>(d[k], 0.f);
+#pragma unroll
+        for (int k = 0; k < R; k++) d[k] += lk_dpp<0x143, 0xC>(d[k], 0.f);
 #pragma unroll
         for (int k = 0; k < R; k++) {
-            if (r0 + k < V) {
-                const float v = lk_wave_sum(row_dot_reg(rr[k], xr, h, lane));
-                if (lane == 0) {
-                    a.logits[r0 + k] = v;
-                    const uint64_t kk = lk_argmax_key(v, r0 + k);
-                    best = kk > best ? kk : best;
-                }
+            const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d[k]), 63));
+            if (r0 + k < V && lane == 0) {
+                a.logits[r0 + k] = v;
+                const uint64_t kk = lk_argmax_key(v, r0 + k);
+                best = kk > best ? kk : best;
             }
         }
     }
