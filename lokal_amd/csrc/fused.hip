@@ -50,6 +50,9 @@
 // gate/up units in flight together in S5 beyond the held ones (Qwen2.5 Q8_0:
 // 2 -> 2319 tok/s, 1 -> 2294; TinyLlama Q4_K: 2 spills, 1347 against 1487)
 #define LKF_XU (WT == LK_Q4_K ? 1 : 2)
+#ifndef LKF_X1
+#define LKF_X1 (WT == LK_Q8_0)
+#endif
 // Stage timestamps of every block (thread 0), kept in LDS and copied out at
 // the end so that tracing adds no global-memory traffic mid-stage;
 // LKF_SUB marks sub-steps of layer 1.
@@ -268,6 +271,11 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         Row<WT, NCHH> orow;                 // issued in S1, used in S4
         Row<WT, NCHH> gq[LKF_KB], uq[LKF_KB];  // issued in S1 (half 1) or S4 (half 0), used in S5
         Row<WT, NCHI> dn;                   // issued in S5, used in S6
+        // the first unit past the held ones of a half-1 wave (which has no
+        // o_proj row): issued in S4 after its input arrived, used in S5
+        const int ux1 = (LKF_KA + LKF_KB) * nwh + (c.gw - nwh);
+        const bool has_x1 = LKF_X1 && half1 && ux1 < (int)U5;
+        Row<WT, NCHH> gx, ux;
         // ---------------- S1: RMSNorm + QKV + bias + RoPE + KV append
         // biases load while the input vector is awaited (held across stages
         // they would be spilled, see rc above)
@@ -564,6 +572,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
             const int u = c.gw;
             stage_in<4>(c, AB + (size_t)cp * qd, qd, ep, xin, -1);
             LKF_SUB(12);
+            if (has_x1) {
+                row_issue(gx, ly.gate, (uint32_t)ux1, lane);
+                row_issue(ux, ly.up, (uint32_t)ux1, lane);
+            }
             if (u < (int)h) {
                 const float d = lk_wave_sum(row_dot(orow, xin, qd, lane));
                 if (lane < (int)rep) publish(XP + (size_t)lane * h + u, xres[u] + d, ep);
@@ -608,12 +620,18 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     if (k < nunits && uu < (int)U5 && lane == 0) publish(IB + uu, gg / (1.0f + expf(-gg)) * up, ep);
                 }
             }
+            if (has_x1) {
+                float gu[2] = {row_dot_reg(gx, xr, h, lane), row_dot_reg(ux, xr, h, lane)};
+                wave_sums(gu);
+                if (lane == 0) publish(IB + ux1, gu[0] / (1.0f + expf(-gu[0])) * gu[1], ep);
+            }
             LKF_SUB(10);
             LKF_SUB(11);
             // wider models: the remaining units, two at a time in flight
             // (Q4_K: one at a time, the second pair of rows would spill)
             constexpr int XU = LKF_XU;
-            for (int uu = (LKF_KA + LKF_KB) * nwh + c.gw; uu < (int)U5; uu += XU * c.nw) {
+            // (with LKF_X1 the first nwh of them went to half 1 in S4)
+            for (int uu = (LKF_KA + LKF_KB) * nwh + c.gw + (LKF_X1 ? nwh : 0); uu < (int)U5; uu += XU * c.nw) {
                 Row<WT, NCHH> gr[XU], pr[XU];
 #pragma unroll
                 for (int x = 0; x < XU; x++) {
