@@ -1455,6 +1455,12 @@ struct lkhip_batch {
     size_t fused_lds[2] = {0, 0};  // 4-row and LK_FUSED_ROWS-row kernels
     uint32_t fused_chunks = 0;
     DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
+    // a step of one row: the single-row one-kernel step (fused.hip) on the
+    // row's cache slot, its own exchange buffers and epoch
+    bool single_ok = false;
+    size_t single_lds = 0;
+    uint32_t single_chunks = 0;
+    DevBuf sxb, sqb, spb, sab, sxpb, sib, sepoch, sxcd;
     std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
     void drop_fused_graphs() {
         for (auto& v : fused_graph) {
@@ -1522,9 +1528,52 @@ static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st
                                 e->fused_blocks, b->fused_lds[nb > 4], st, false);
 }
 
+// One row's decode step on the single-row one-kernel step: token, position and
+// cache slot from row 0 of the row table on the device, the final x into
+// rows.x for the rows' lm_head.
+static hipError_t batch_enqueue_single(lkhip_batch* b, hipStream_t st) {
+    const lkhip_engine* e = b->e;
+    const lkhip_config& c = e->cfg;
+    LkFusedArgs a{};
+    a.layers = e->fused_layers.as<LkFusedLayer>();
+    a.n_layers = c.num_hidden_layers;
+    a.embed = e->embed->dw;
+    a.norm = e->norm.as<float>();
+    a.freq = e->freq;
+    a.h = c.hidden_size;
+    a.I = c.intermediate_size;
+    a.nh = c.num_attention_heads;
+    a.nkv = c.num_key_value_heads;
+    a.vocab = c.vocab_size;
+    a.eps = c.rms_norm_eps;
+    a.kc = b->kv.kc;
+    a.vc = b->kv.vc;
+    a.kv_layer = b->kv.layer_bytes / 2;
+    a.max_seq = b->kv.kv_seq;
+    a.max_chunks = b->single_chunks;
+    a.epoch = b->sepoch.as<uint32_t>();
+    a.err = b->ferr.as<uint32_t>();
+    a.xcd_cnt = b->sxcd.as<uint32_t>();
+    a.xb = b->sxb.as<uint64_t>();
+    a.qb = b->sqb.as<uint64_t>();
+    a.pb = b->spb.as<uint64_t>();
+    a.ab = b->sab.as<uint64_t>();
+    a.xpb = b->sxpb.as<uint64_t>();
+    a.ib = b->sib.as<uint64_t>();
+    a.rep = LK_XCDS;
+    a.meta = b->rows.meta.as<uint32_t>();
+    a.meta_cap = b->rows.cap;
+    a.nrows = 1;
+    a.slot_elems = b->kv.slot_elems;
+    a.x_out = b->rows.x.as<float>();
+    return lk_fused_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, 0, e->fused_blocks,
+                           b->single_lds, st, false);
+}
+
 // Whether the one-kernel step takes rows at these positions (the largest of
 // each row over the call): one wave per (row, head, 64-position tile).
 static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
+    if (last_pos.size() == 1 && b->single_ok) return true;  // the single-row step (any position)
     if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS) return false;
     const lkhip_config& c = b->e->cfg;
     const size_t nb = last_pos.size() <= 4 ? 4 : LK_FUSED_ROWS;
@@ -1543,7 +1592,8 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, bool fuse
     std::vector<hipGraphExec_t>& cache =
         fused ? b->fused_graph[greedy ? 1 : 0] : (greedy ? b->greedy_graph : b->step_graph);
     auto body = [&](hipStream_t st) -> hipError_t {
-        hipError_t err = fused ? batch_enqueue_fused(b, n, st) : enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        hipError_t err = !fused ? enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st)
+                                : (n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st));
         if (err == hipSuccess && fused) err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;
         return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
@@ -1636,6 +1686,27 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
             (void)hipGetLastError();
         }
     }
+    // steps of one row: the single-row one-kernel step, for any cache length
+    // it takes (LKHIP_BATCH_FUSED=0 keeps these on the per-layer launches too)
+    if (e->fused_ok && !(fe && fe[0] == '0') && kv_seq <= LK_FUSED_MAX_SEQ) {
+        const size_t h = c.hidden_size, I = c.intermediate_size;
+        const size_t qkvd = e->qd + 2 * e->kvd;
+        b->single_chunks = (uint32_t)std::min<size_t>(kv_seq / 64, LK_FUSED_MAX_CH);
+        b->single_lds = lk_fused_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads,
+                                           c.num_key_value_heads, (uint32_t)e->fused_g, b->single_chunks);
+        if ((rc = dev_alloc(b->sxb, 2 * h * 8 * LK_FUSED_REP)) || (rc = dev_alloc(b->sqb, 2 * LK_XCDS * qkvd * 8)) ||
+            (rc = dev_alloc(b->spb, 2 * (size_t)c.num_attention_heads * b->single_chunks * 66 * 8)) ||
+            (rc = dev_alloc(b->sab, 2 * (size_t)e->qd * 8 * LK_FUSED_REP)) ||
+            (rc = dev_alloc(b->sxpb, 2 * h * 8 * LK_FUSED_REP)) || (rc = dev_alloc(b->sib, 2 * I * 8)) ||
+            (rc = dev_alloc(b->sepoch, 4)) || (rc = dev_alloc(b->sxcd, LK_XCDS * LK_XCD_CNT_STRIDE * 4)))
+            return rc;
+        if (!b->ferr.p && (rc = dev_alloc(b->ferr, 4))) return rc;
+        HIP_OR_FAIL(hipMemset(b->sxcd.p, 0, LK_XCDS * LK_XCD_CNT_STRIDE * 4));
+        HIP_OR_FAIL(hipMemset(b->ferr.p, 0, 4));
+        const uint32_t one = 1;
+        HIP_OR_FAIL(hipMemcpy(b->sepoch.p, &one, 4, hipMemcpyHostToDevice));
+        b->single_ok = true;
+    }
     *out = b.release();
     return LKHIP_OK;
 }
@@ -1651,6 +1722,7 @@ static int batch_sync_check(lkhip_batch* b, bool fused) {
     if (!flag) return LKHIP_OK;
     HIP_OR_FAIL(hipMemset(b->ferr.p, 0, 4));
     b->fused_ok = false;
+    b->single_ok = false;
     b->drop_fused_graphs();
     return fail(LKHIP_E_HIP, "the multi-row one-kernel step timed out waiting on another workgroup (is every CU "
                              "free?) — this batcher now runs the per-layer kernels; repeat the call");

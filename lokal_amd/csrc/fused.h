@@ -46,9 +46,11 @@ struct LkFusedArgs {
     // published (1..LK_FUSED_REP); each workgroup polls copy blockIdx % rep.
     // xb, ab and xpb hold [2][LK_FUSED_REP][n] words.
     uint32_t rep;
-    // Batcher rows (fused_rows.hip only): meta = u32 [ids | pos | slots | ...],
-    // meta_cap apart; nrows live rows; slot_elems = KV elements between two
-    // slots; x_out = the final layer's f32 rows [nrows][h]
+    // Batcher rows: meta = u32 [ids | pos | slots | ...], meta_cap apart;
+    // nrows live rows; slot_elems = KV elements between two slots; x_out = the
+    // final layer's f32 rows [nrows][h].  fused_rows.hip reads nrows rows;
+    // fused.hip, when meta is set, serves row 0 from it (token, position and
+    // KV slot) instead of st and writes x_out.
     const uint32_t* meta;
     uint32_t meta_cap, nrows;
     uint64_t slot_elems;

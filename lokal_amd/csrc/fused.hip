@@ -142,8 +142,21 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     constexpr bool KV32 = sizeof(KV) == 4;
     constexpr int KC = KV32 ? 16 : 8;  // 16-byte chunks in a 64-element cache row
     const uint32_t base = a.epoch[0];
-    const LkStepState st = *a.st;
-    const uint32_t pos = st.pos, token = st.token;
+    // the step's token and position: the session's device state, or (a
+    // Batcher row, meta set) row 0 of the Batcher's row table, whose cache
+    // slot selects the KV rows
+    uint32_t pos, token, slot = 0;
+    if (a.meta) {
+        token = __builtin_amdgcn_readfirstlane(a.meta[0]);
+        pos = __builtin_amdgcn_readfirstlane(a.meta[a.meta_cap]);
+        slot = __builtin_amdgcn_readfirstlane(a.meta[2 * a.meta_cap]);
+    } else {
+        const LkStepState st = *a.st;
+        pos = st.pos;
+        token = st.token;
+    }
+    KV* const kc0 = (KV*)a.kc + (size_t)slot * a.slot_elems;
+    KV* const vc0 = (KV*)a.vc + (size_t)slot * a.slot_elems;
     const uint32_t nL = a.n_layers;
     const float fpos = (float)pos;
     const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
@@ -293,8 +306,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         const uint32_t j = hq / G;
         const uint32_t t0 = ck * tpw, t1 = t0 + tpw < ntile ? t0 + tpw : ntile;
         const bool chunk_cur = t1 == ntile;  // the chunk holding position pos
-        const KV* K = (const KV*)a.kc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
-        const KV* V = (const KV*)a.vc + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+        const KV* K = kc0 + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
+        const KV* V = vc0 + (size_t)L * a.kv_layer + (size_t)j * a.max_seq * 64;
         const uint32_t sub = (uint32_t)lane & 7, dq = ((uint32_t)lane >> 3) * 8;
         // Cached positions (< pos) do not depend on this token: the first
         // tile is loaded before the wait for q.  The cache holds whole
@@ -345,7 +358,7 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     publish_x(QB + r + 32, d2, ep);
                 } else {
                     if (kv_writer) {
-                        KV* cache = (KV*)(kind == 1 ? a.kc : a.vc) + (size_t)L * a.kv_layer +
+                        KV* cache = (kind == 1 ? kc0 : vc0) + (size_t)L * a.kv_layer +
                                     ((size_t)head * a.max_seq + pos) * 64;
                         kv_put(cache + ip, d1);
                         kv_put(cache + ip + 32, d2);
@@ -669,12 +682,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 const float d = lk_wave_sum(row_dot(dn, xin, I, lane));
                 LKF_SUB(19);
                 if (lane < (int)rep) publish(XN + (size_t)lane * h + c.gw, xres[c.gw] + d, epn);
+                if (a.x_out && L + 1 == nL && lane == 0) a.x_out[c.gw] = xres[c.gw] + d;  // a Batcher row's final x
             }
             for (int uu = c.gw + c.nw; uu < (int)h; uu += c.nw) {
                 Row<WT, NCHI> rr;
                 row_issue(rr, ly.down, (uint32_t)uu, lane);
                 const float d = lk_wave_sum(row_dot(rr, xin, I, lane));
                 if (lane < (int)rep) publish(XN + (size_t)lane * h + uu, xres[uu] + d, epn);
+                if (a.x_out && L + 1 == nL && lane == 0) a.x_out[uu] = xres[uu] + d;
             }
             if (L + 1 < nL) {  // read after the next stage_in's barrier
                 gains_issue(lay[L + 1]);
