@@ -275,8 +275,8 @@ def test_batcher_refusals():
 @pytest.mark.parametrize("kind", ["q8_0", "f16"])
 @pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 8])
 def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
-    """The multi-row one-kernel step at 1-8 rows (4- and 8-row kernels, fewer
-    rows padded), on slots other than 0..n-1: every row against the oracle
+    """The one-kernel Batcher step at 1-8 rows (1 row: the single-row kernel;
+    2-8 rows: the 4- and 8-row kernels, fewer rows padded), on slots other than 0..n-1: every row against the oracle
     over steps that cross a 64-position tile, then greedy ids against the
     oracle's."""
     monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
@@ -307,6 +307,49 @@ def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
         agree = next((k for k in range(12) if ids[k, i] != want[k]), 12)
         print(f"{kind} rows={n_rows} row {i}: {agree}/12 greedy ids agree with the CPU path")
         assert agree >= 6
+    bat.close()
+    eng.close()
+    om.close()
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+def test_batcher_one_row_steps_mixed_with_multi_row_steps_and_a_session(kind, monkeypatch):
+    """A 1-row decode_step runs the single-row one-kernel step on the
+    Batcher's row table (token, position, KV slot); it interleaves with
+    multi-row steps on the same slots and with a Session of the same engine
+    stepping in between, and every row stays equal to the oracle's own
+    sequence (src/engine.rs:42-47)."""
+    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
+    cfg, eng, om = build(kind, seed=21)
+    rng = np.random.default_rng(21)
+    lens = [70, 2, 33]
+    slots = [5, 0, 3]
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    bat = eng.batcher(6, 160)
+    orc = [om.session(160, kv_f16=True) for _ in lens]
+    for i, p in enumerate(prompts):
+        bat.prefill(slots[i], p)
+        orc[i].prefill(p)
+    sp = rng.integers(0, cfg.vocab_size, 9).astype(np.uint32)
+    ses = eng.session(160)
+    so = om.session(160, kv_f16=True)
+    ses.prefill(sp)
+    so.prefill(sp)
+    spos = len(sp)
+    pos = list(lens)
+    # 1 row, all rows, 1 row of another slot, 2 rows, 1 row ...
+    plan = [[0], [0, 1, 2], [2], [1, 0], [1], [2], [0, 2], [0]]
+    for step, which in enumerate(plan):
+        toks = {i: int(rng.integers(0, cfg.vocab_size)) for i in which}
+        outs = bat.decode_step([BatchRow(toks[i], pos[i], slots[i]) for i in which])
+        for i, out in zip(which, outs):
+            assert rel_err(out, orc[i].forward(toks[i], pos[i])) < TOL_F16_KV, (step, i)
+            pos[i] += 1
+        t = int(rng.integers(0, cfg.vocab_size))
+        assert rel_err(ses.forward(t, spos), so.forward(t, spos)) < TOL_F16_KV, step
+        spos += 1
+    ses.close()
+    so.close()
     bat.close()
     eng.close()
     om.close()
