@@ -1452,7 +1452,7 @@ struct lkhip_batch {
     std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
     // the multi-row one-kernel step (fused_rows.hip) for up to LK_FUSED_ROWS rows
     bool fused_ok = false;
-    size_t fused_lds[2] = {0, 0};  // 4-row and LK_FUSED_ROWS-row kernels
+    size_t fused_lds[3] = {0, 0, 0};  // 2-row, 4-row and LK_FUSED_ROWS-row kernels
     uint32_t fused_chunks = 0;
     DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
     // a step of one row: the single-row one-kernel step (fused.hip) on the
@@ -1490,6 +1490,11 @@ static bool graphs_on() {
 
 // The multi-row one-kernel step over the rows whose meta is on the device,
 // leaving the final x rows in rows.x.
+// Rows of the multi-row one-kernel step's instances, and the one that serves
+// n rows (fewer are padded).
+static constexpr uint32_t kRowsNb[3] = {2, 4, LK_FUSED_ROWS};
+static int rows_kernel(size_t n) { return n <= 2 ? 0 : n <= 4 ? 1 : 2; }
+
 static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st) {
     const lkhip_engine* e = b->e;
     const lkhip_config& c = e->cfg;
@@ -1523,9 +1528,9 @@ static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st
     a.nrows = n;
     a.slot_elems = b->kv.slot_elems;
     a.x_out = b->rows.x.as<float>();
-    const uint32_t nb = n <= 4 ? 4 : LK_FUSED_ROWS;
-    return lk_fused_rows_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, nb,
-                                e->fused_blocks, b->fused_lds[nb > 4], st, false);
+    const int k = rows_kernel(n);
+    return lk_fused_rows_launch(a, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g,
+                                kRowsNb[k], e->fused_blocks, b->fused_lds[k], st, false);
 }
 
 // One row's decode step on the single-row one-kernel step: token, position and
@@ -1576,7 +1581,7 @@ static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& la
     if (last_pos.size() == 1 && b->single_ok) return true;  // the single-row step (any position)
     if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS) return false;
     const lkhip_config& c = b->e->cfg;
-    const size_t nb = last_pos.size() <= 4 ? 4 : LK_FUSED_ROWS;
+    const size_t nb = kRowsNb[rows_kernel(last_pos.size())];
     size_t items = (nb - last_pos.size()) * c.num_attention_heads;  // padding rows
     for (size_t p : last_pos) {
         if (p / 64 + 1 > b->fused_chunks) return false;
@@ -1666,8 +1671,8 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         b->fused_chunks = (uint32_t)(kv_seq / 64);
         LkFusedArgs probe{};
         bool ok = true;
-        for (int k = 0; k < 2 && ok; k++) {
-            const uint32_t kb = k ? LK_FUSED_ROWS : 4;
+        for (int k = 0; k < 3 && ok; k++) {
+            const uint32_t kb = kRowsNb[k];
             b->fused_lds[k] = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, kb);
             ok = lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, kb,
                                       e->fused_blocks, b->fused_lds[k], nullptr, true) == hipSuccess;

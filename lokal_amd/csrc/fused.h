@@ -76,8 +76,9 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 #define LK_FUSED_ROWS_MAX_SEQ 4096u
 // Exchange-vector copies the single-row step's buffers are laid out for.
 #define LK_FUSED_REP 8u
-// XCDs of the part (workgroup b runs on XCD b % LK_XCDS) and the hardware
-// register holding a wave's XCD id (s_getreg_b32 HW_REG_XCC_ID, bits 3:0).
+// XCDs of the part (a launch's workgroups are dealt to them in turn, from an
+// XCD that depends on earlier launches) and the hardware register holding a
+// wave's XCD id (s_getreg_b32 HW_REG_XCC_ID, bits 3:0).
 #define LK_XCDS 8u
 #define LK_XCD_CNT_STRIDE 64u
 #define LK_HWREG_XCC_ID (20 | (0 << 6) | ((4 - 1) << 11))
@@ -87,8 +88,8 @@ size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uin
 int lk_fused_threads();
 // Writes the XCD id (0..15) of each workgroup of a `blocks`-workgroup launch.
 hipError_t lk_xcd_probe_launch(uint32_t* out, unsigned blocks, hipStream_t st);
-// The multi-row one-kernel step (fused_rows.hip): 4 or LK_FUSED_ROWS Batcher
-// rows per launch (fewer are padded), f16 KV.
+// The multi-row one-kernel step (fused_rows.hip): 2, 4 or LK_FUSED_ROWS
+// Batcher rows per launch (fewer are padded), f16 KV.
 #define LK_FUSED_ROWS 8u
 size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb);
 hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, uint32_t nb,

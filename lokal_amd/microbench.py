@@ -348,7 +348,7 @@ def batch() -> list[dict]:
     rng = np.random.default_rng(12)
     out = []
     steps = 64
-    for B in (1, 4, 8, 16, 64):
+    for B in (1, 2, 3, 4, 8, 16, 64):
         bat = eng.batcher(B, 512 + steps + 16)
         first = []
         for slot in range(B):

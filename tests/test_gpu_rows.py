@@ -276,9 +276,9 @@ def test_batcher_refusals():
 @pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 8])
 def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
     """The one-kernel Batcher step at 1-8 rows (1 row: the single-row kernel;
-    2-8 rows: the 4- and 8-row kernels, fewer rows padded), on slots other than 0..n-1: every row against the oracle
-    over steps that cross a 64-position tile, then greedy ids against the
-    oracle's."""
+    2-8 rows: the 2-, 4- and 8-row kernels, fewer rows padded), on slots
+    other than 0..n-1: every row against the oracle over steps that cross a
+    64-position tile, then greedy ids against the oracle's."""
     monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
     cfg, eng, om = build(kind, seed=10 + n_rows)
     rng = np.random.default_rng(n_rows)
