@@ -273,7 +273,7 @@ def test_batcher_refusals():
 
 
 @pytest.mark.parametrize("kind", ["q8_0", "f16"])
-@pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
     """The one-kernel Batcher step at 1-8 rows (1 row: the single-row kernel;
     2-8 rows: the 2-, 4- and 8-row kernels, fewer rows padded), on slots
