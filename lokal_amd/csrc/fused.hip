@@ -639,6 +639,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 if (lane == 0) publish(IB + ux1, gu[0] / (1.0f + expf(-gu[0])) * gu[1], ep);
             }
             LKF_SUB(10);
+            if (L == 1 && tracing && threadIdx.x == FT - 64)  // the block's last wave (half 1)
+                ltr[2 + 6 * nL + 1 + 22] = __builtin_amdgcn_s_memrealtime();
             LKF_SUB(11);
             // wider models: the remaining units, two at a time in flight
             // (Q4_K: one at a time, the second pair of rows would spill)

@@ -195,7 +195,8 @@ def stage_trace(name: str = "qwen2.5-0.5b-q8_0", prompt_len: int = 512) -> list[
     subs = {15: "S1 x in", 17: "S1 dots", 18: "S1 published", 1: "S2 tile issued", 2: "S2 q arrived",
             3: "S2 scores", 4: "S2 softmax", 5: "S2 P.V", 6: "S2 published", 20: "S3 partials in",
             21: "S3 published", 12: "S4 input in", 13: "S4 published", 14: "S4 rows issued", 8: "S5 input in",
-            9: "S5 norm", 10: "S5 held units", 7: "S6 input in", 19: "S6 dot"}
+            9: "S5 norm", 10: "S5 held units", 22: "S5 units of the last wave", 7: "S6 input in",
+            19: "S6 dot"}
     ref = u[:, 2 + 5].max()
     for k, nm in subs.items():
         v = t[:, 2 + 6 * L + 1 + k]
