@@ -1729,7 +1729,7 @@ static int batch_sync_check(lkhip_batch* b, bool fused) {
     b->fused_ok = false;
     b->single_ok = false;
     b->drop_fused_graphs();
-    return fail(LKHIP_E_HIP, "the multi-row one-kernel step timed out waiting on another workgroup (is every CU "
+    return fail(LKHIP_E_HIP, "the batcher's one-kernel step timed out waiting on another workgroup (is every CU "
                              "free?) — this batcher now runs the per-layer kernels; repeat the call");
 }
 extern "C" void lkhip_batch_destroy(lkhip_batch* b) { delete b; }
