@@ -1553,7 +1553,7 @@ static hipError_t batch_enqueue_single(lkhip_batch* b, hipStream_t st) {
     a.eps = c.rms_norm_eps;
     a.kc = b->kv.kc;
     a.vc = b->kv.vc;
-    a.kv_layer = b->kv.layer_bytes / 2;
+    a.kv_layer = b->kv.layer_bytes / sizeof(uint16_t);  // a Batcher's cache is f16
     a.max_seq = b->kv.kv_seq;
     a.max_chunks = b->single_chunks;
     a.epoch = b->sepoch.as<uint32_t>();
@@ -1716,9 +1716,9 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
     return LKHIP_OK;
 }
 
-// Waits for the batch stream; if a bounded wait inside the multi-row
-// one-kernel step timed out, the batcher drops to the per-layer launches and
-// the call fails (repeating it recomputes the same positions).
+// Waits for the batch stream; if a bounded wait inside a one-kernel step
+// (single- or multi-row) timed out, the batcher drops to the per-layer
+// launches and the call fails (repeating it recomputes the same positions).
 static int batch_sync_check(lkhip_batch* b, bool fused) {
     HIP_OR_FAIL(hipStreamSynchronize(b->stream));
     if (!fused) return LKHIP_OK;
