@@ -828,7 +828,8 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
     if (e->fused_ok && max_seq <= LK_FUSED_MAX_SEQ) {
         const size_t h = c.hidden_size, I = c.intermediate_size;
         const size_t qkvd = e->qd + 2 * e->kvd;
-        s->max_chunks = (uint32_t)std::min<size_t>((max_seq + 63) / 64, LK_FUSED_MAX_CH);
+        const size_t unit = lk_fused_unit(s->kv_f32 != 0);
+        s->max_chunks = (uint32_t)std::min<size_t>((max_seq + unit - 1) / unit, LK_FUSED_MAX_CH);
         if ((rc = dev_alloc(s->xb, 2 * h * 8 * LK_FUSED_REP)) || (rc = dev_alloc(s->qb, 2 * LK_XCDS * qkvd * 8)) ||
             (rc = dev_alloc(s->pb, 2 * (size_t)c.num_attention_heads * s->max_chunks * 66 * 8)) ||
             (rc = dev_alloc(s->ab, 2 * (size_t)e->qd * 8 * LK_FUSED_REP)) ||

@@ -32,7 +32,7 @@ struct LkFusedArgs {
     // exchange buffers of (f32 | epoch) words, two copies by layer parity
     uint64_t* xb;   // [2][h]        layer input x
     uint64_t* qb;   // [2][qd+2kvd]  rotated q, this token's k and v
-    uint64_t* pb;   // [2][nh][max_chunks][66] attention partials of each 64-position tile (m, l, acc[64])
+    uint64_t* pb;   // [2][nh][max_chunks][66] attention partials of each chunk (m, l, acc[64])
     uint64_t* ab;   // [2][qd]       attention output
     uint64_t* xpb;  // [2][h]        x after the attention residual
     uint64_t* ib;   // [2][I]        SwiGLU output
@@ -68,10 +68,13 @@ __host__ __device__ inline uint32_t lk_fused_trace_len(uint32_t n_layers) { retu
 size_t lk_fused_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nkv, uint32_t G, uint32_t max_chunks);
 // Longest session (positions) the one-kernel step serves; longer ones run the
 // per-stage kernels.  A head's attention is split into at most
-// LK_FUSED_MAX_CH chunks of whole 64-position tiles (one per lane of the
-// merge), each chunk one wave.
+// LK_FUSED_MAX_CH chunks of whole attention units (lk_fused_unit; one chunk
+// per lane of the merge), each chunk one wave.
 #define LK_FUSED_MAX_SEQ 32768u
 #define LK_FUSED_MAX_CH 64u
+// Positions of the one-kernel step's attention unit (a chunk is a run of
+// whole units): a 64-position cache tile, half of one with an f32 cache.
+__host__ __device__ constexpr uint32_t lk_fused_unit(bool kv_f32) { return kv_f32 ? 32u : 64u; }
 // Longest session of the multi-row one-kernel step (one tile per wave).
 #define LK_FUSED_ROWS_MAX_SEQ 4096u
 // Exchange-vector copies the single-row step's buffers are laid out for.

@@ -159,7 +159,10 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     KV* const vc0 = (KV*)a.vc + (size_t)slot * a.slot_elems;
     const uint32_t nL = a.n_layers;
     const float fpos = (float)pos;
-    const uint32_t ntile = pos / 64 + 1;            // 64-position tiles holding positions 0..pos
+    // attention unit: a 64-position cache tile, or half of one with an f32
+    // cache (a whole f32 tile's K and V would take 128 registers per lane)
+    constexpr uint32_t UNIT = lk_fused_unit(KV32);
+    const uint32_t ntile = pos / UNIT + 1;          // units holding positions 0..pos
     // attention items: (query head, chunk of tpw consecutive tiles), one wave
     // each; tpw grows with the context so a head never has more than
     // LK_FUSED_MAX_CH chunks (S3 holds one chunk per lane)
@@ -314,21 +317,24 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         // 64-position tiles (its per-head stride is max_seq rounded up to
         // 64), so every row of a tile is in bounds; rows >= pos are
         // replaced (pos) or masked (> pos) below.
-        uint4 kraw[KC], vraw[KC];
+        // a unit's K and V per wave; with 32-position units lanes l and l + 32
+        // hold the two halves of a position's dims (K)
+        constexpr int KH = UNIT == 64 ? KC : KC / 2;
+        uint4 kraw[KH], vraw[KH];
         // K rows from pos on are this token's (in flight from S1) or
         // unwritten: read row pos - 1 instead (the lane's score is
         // replaced or masked below)
         auto load_k = [&](uint32_t t) {
-            uint32_t krow = t * 64u + (uint32_t)lane;
+            uint32_t krow = t * UNIT + ((uint32_t)lane & (UNIT - 1));
             krow = krow < pos ? krow : (pos ? pos - 1 : 0);
-            const KV* Kl = K + krow * 64u;
+            const KV* Kl = K + krow * 64u + (UNIT == 64 ? 0u : 32u * ((uint32_t)lane >> 5));
 #pragma unroll
-            for (int q = 0; q < KC; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
+            for (int q = 0; q < KH; q++) kraw[q] = *(const uint4*)((const uint8_t*)Kl + 16 * q);
         };
         auto load_v = [&](uint32_t t) {
-            const KV* Vl = V + (t * 64u + sub) * 64u + dq;
+            const KV* Vl = V + (t * UNIT + sub) * 64u + dq;
 #pragma unroll
-            for (int q = 0; q < KC; q++)
+            for (int q = 0; q < KH; q++)
                 vraw[q] = *(const uint4*)(Vl + (KV32 ? (q / 2) * 8 * 64 + (q & 1) * 4 : q * 8 * 64));
         };
         // f16: a tile's K and V fit in registers together; f32: V follows the scores
@@ -424,8 +430,9 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     wave_sync_lds();  // the previous tile's weight reads are done
                     load_tile(t);
                 }
-                const bool has_cur = t + 1 == ntile;  // the tile holding position pos
-                const uint32_t p = t * 64 + (uint32_t)lane;
+                const bool has_cur = t + 1 == ntile;  // the unit holding position pos
+                const uint32_t p = t * UNIT + ((uint32_t)lane & (UNIT - 1));
+                const bool own = UNIT == 64 || lane < 32;  // 32-position units: lanes 32.. repeat positions
                 const bool valid = p <= pos;
                 // this token's k (lane p == pos) comes from LDS: its cache row
                 // is being written in this stage.  Selected per value rather
@@ -435,18 +442,20 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 // four independent chains: one wave per SIMD has nothing to
                 // hide a 64-long dependent FMA chain behind
                 float s4[4] = {0.f, 0.f, 0.f, 0.f};
+                const float* wqh = wq + (UNIT == 64 ? 0 : 32 * (lane >> 5));
 #pragma unroll
-                for (int q = 0; q < 8; q++) {  // 8 dims at a time
+                for (int q = 0; q < (UNIT == 64 ? 8 : 4); q++) {  // 8 dims at a time
                     float k8[8];
                     unpack8(kraw, q, KV32, k8);
-                    const float4 qa = *(const float4*)(wq + 8 * q);
-                    const float4 qb = *(const float4*)(wq + 8 * q + 4);
+                    const float4 qa = *(const float4*)(wqh + 8 * q);
+                    const float4 qb = *(const float4*)(wqh + 8 * q + 4);
                     s4[0] = fmaf(k8[0], qa.x, s4[0]); s4[1] = fmaf(k8[1], qa.y, s4[1]);
                     s4[2] = fmaf(k8[2], qa.z, s4[2]); s4[3] = fmaf(k8[3], qa.w, s4[3]);
                     s4[0] = fmaf(k8[4], qb.x, s4[0]); s4[1] = fmaf(k8[5], qb.y, s4[1]);
                     s4[2] = fmaf(k8[6], qb.z, s4[2]); s4[3] = fmaf(k8[7], qb.w, s4[3]);
                 }
                 float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+                if constexpr (UNIT == 32) s += __shfl_xor(s, 32);  // the other 32 dims (lane +- 32)
                 if (has_cur) {  // wave-uniform: lane = dim, then the wave sum
                     const float sc = lk_wave_sum(wk[lane] * wq[lane]);
                     if (cur) s = sc;
@@ -456,24 +465,32 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                 // the tile's part of math::softmax (src/math.rs:55-66), folded
                 // into the chunk's running max and sum; chunks are combined in
                 // S3 with the same split-invariant rescaling
-                const float sg = valid ? s * 0.125f : -INFINITY;
-                const float mn = fmaxf(m, lk_wave_max(sg));  // finite: the tile holds position <= pos
-                const float fo = expf(m - mn);                // 0 on the chunk's first tile
-                const float pe = valid ? expf(sg - mn) : 0.f;
+                const float sg = valid && own ? s * 0.125f : -INFINITY;
+                const float mn = fmaxf(m, lk_wave_max(sg));  // finite: the unit holds position <= pos
+                const float fo = expf(m - mn);                // 0 on the chunk's first unit
+                const float pe = valid && own ? expf(sg - mn) : 0.f;
                 l = fmaf(l, fo, lk_wave_sum(pe));
                 m = mn;
 #pragma unroll
                 for (int e = 0; e < 8; e++) acc[e] *= fo;
-                wP[(lane & 7) * 8 + (lane >> 3)] = pe;  // [group][jj]: a lane's 8 weights are adjacent
+                constexpr int NJ = UNIT / 8;  // positions per lane in P.V (position groups of 8)
+                if (own) wP[(lane & 7) * NJ + (lane >> 3)] = pe;  // [group][jj]: a lane's weights are adjacent
                 wave_sync_lds();
                 LKF_SUB(4);
-                // this lane's 8 weights in two LDS reads; no per-position
-                // branches (each would serialise an LDS round trip)
-                const float4 pwa = *(const float4*)(wP + sub * 8), pwb = *(const float4*)(wP + sub * 8 + 4);
-                const float pw8[8] = {pwa.x, pwa.y, pwa.z, pwa.w, pwb.x, pwb.y, pwb.z, pwb.w};
-                if (!has_cur) {  // wave-uniform: every position of the tile is < pos
+                // this lane's NJ weights in one or two LDS reads; no
+                // per-position branches (each would serialise an LDS round trip)
+                float pw8[NJ];
+                {
+                    const float4 pwa = *(const float4*)(wP + sub * NJ);
+                    pw8[0] = pwa.x; pw8[1] = pwa.y; pw8[2] = pwa.z; pw8[3] = pwa.w;
+                    if constexpr (NJ == 8) {
+                        const float4 pwb = *(const float4*)(wP + sub * NJ + 4);
+                        pw8[4] = pwb.x; pw8[5] = pwb.y; pw8[6] = pwb.z; pw8[7] = pwb.w;
+                    }
+                }
+                if (!has_cur) {  // wave-uniform: every position of the unit is < pos
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) {
+                    for (int jj = 0; jj < NJ; jj++) {
                         float v8[8];
                         unpack8(vraw, jj, KV32, v8);
 #pragma unroll
@@ -485,8 +502,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
                     const float4 va = *(const float4*)(wvc + dq), vb = *(const float4*)(wvc + dq + 4);
                     const float vc8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) {
-                        const uint32_t pj = t * 64 + jj * 8 + sub;
+                    for (int jj = 0; jj < NJ; jj++) {
+                        const uint32_t pj = t * UNIT + jj * 8 + sub;
                         float v8[8];
                         unpack8(vraw, jj, KV32, v8);
                         const float pw = pj <= pos ? pw8[jj] : 0.f;
