@@ -1,7 +1,7 @@
 """Measurements of the decode-step kernels on the workloads other than the
 headline one (bench.py measures config 3, Qwen2.5-0.5B-shape Q8_0 decode).
 
-    python -m lokal_amd.microbench [--only decode,layers,attn,gemm,prefill,batch]
+    python -m lokal_amd.microbench [--only decode,longctx,layers,attn,gemm,prefill,batch]
 
 Prints one JSON object per measurement:
   decode  configs 1 and 4: SmolLM2-135M-shape F16 (512-token prompt, 128
@@ -478,6 +478,9 @@ def main() -> int:
     if "decode" in want:
         print(json.dumps(decode("smollm2-135m", 512, 128)), flush=True)
         print(json.dumps(decode("tinyllama-1.1b-q4_k", 256, 256)), flush=True)
+    if "longctx" in want:  # the one-kernel step at long contexts (up to LK_FUSED_MAX_SEQ)
+        for p in (4096, 16384, 32000):
+            print(json.dumps(decode("qwen2.5-0.5b-q8_0", p, 64)), flush=True)
     if "layers" in want:
         for r in layers():
             print(json.dumps(r), flush=True)
