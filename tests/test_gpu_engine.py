@@ -331,3 +331,30 @@ def test_two_sessions_stepping_from_two_threads_match_their_solo_runs():
     for s in sessions:
         s.close()
     eng.close()
+
+
+@pytest.mark.parametrize("path", ["fused", "stages"])
+def test_graph_replay_matches_direct_launches(path, monkeypatch):
+    """LKHIP_GRAPH=1 replays a session's step as a HIP graph (by default the
+    one-kernel step is launched directly, the per-stage step replayed);
+    LKHIP_GRAPH=0 launches it directly.  Both give the same greedy ids and
+    the same logits bit for bit, over three decode calls with host work and
+    synchronisation between the replays."""
+    cfg, tensors, eng, om = build("q8_0", path, seed=31)
+    prompt = np.random.default_rng(31).integers(0, cfg.vocab_size, 40).astype(np.uint32)
+    runs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LKHIP_GRAPH", mode)
+        s = eng.session(160)
+        first = int(np.argmax(s.prefill(prompt)))
+        ids, pos, lg = [], len(prompt), None
+        for _ in range(3):
+            got, lg = s.decode_greedy(first, pos, 16, want_logits=True)
+            ids += [int(t) for t in got]
+            first, pos = int(got[-1]), pos + 16
+        runs[mode] = (ids, lg.copy())
+        s.close()
+    assert runs["1"][0] == runs["0"][0]
+    assert np.array_equal(runs["1"][1], runs["0"][1])
+    eng.close()
+    om.close()
