@@ -775,16 +775,13 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
     return hipSuccess;
 }
 
-// Whether the session replays its step as a HIP graph.  The per-stage step
-// is ~220 launches and gains from one; the one-kernel step is two, and
-// launching them directly measured faster than replaying a graph of the two
-// (Qwen2.5 shape: 2590 against 2555 tok/s).  LKHIP_GRAPH=0 never uses a
-// graph (tools that cannot follow graph launches), LKHIP_GRAPH=1 always does.
-static bool want_graph(const lkhip_session* s) {
+// Whether the session replays its step as a HIP graph (LKHIP_GRAPH=1).  By
+// default it launches the step directly: measured on MI355X at the Qwen2.5
+// shape, the one-kernel step's two launches ran faster that way (2590 against
+// 2555 tok/s) and the per-stage step's ~220 as fast (1177 against 1172).
+static bool want_graph(const lkhip_session*) {
     const char* g = getenv("LKHIP_GRAPH");
-    if (g && g[0] == '0') return false;
-    if (g && g[0] == '1') return true;
-    return !s->use_fused;
+    return g && g[0] == '1';
 }
 
 static int build_graph(lkhip_session* s) {

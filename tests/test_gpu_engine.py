@@ -335,9 +335,8 @@ def test_two_sessions_stepping_from_two_threads_match_their_solo_runs():
 
 @pytest.mark.parametrize("path", ["fused", "stages"])
 def test_graph_replay_matches_direct_launches(path, monkeypatch):
-    """LKHIP_GRAPH=1 replays a session's step as a HIP graph (by default the
-    one-kernel step is launched directly, the per-stage step replayed);
-    LKHIP_GRAPH=0 launches it directly.  Both give the same greedy ids and
+    """LKHIP_GRAPH=1 replays a session's step as a HIP graph; by default
+    (here LKHIP_GRAPH=0) it is launched directly.  Both give the same greedy ids and
     the same logits bit for bit, over three decode calls with host work and
     synchronisation between the replays."""
     cfg, tensors, eng, om = build("q8_0", path, seed=31)
