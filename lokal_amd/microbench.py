@@ -187,6 +187,11 @@ def stage_trace(name: str = "qwen2.5-0.5b-q8_0", prompt_len: int = 512) -> list[
     per_layer = (u[:, 2 + 6 * (L - 1) + 5].max() - u[:, 2 + 6 * 0 + 5].max()) / (L - 1)
     out = [{"workload": "stage-trace", "model": name, "position": prompt_len + 16, "workgroups": int(t.shape[0]),
             "us_per_layer": round(per_layer, 2)}]
+    # the launch's start: when the workgroups began (from the first one), when
+    # each had the token's embedding, when layer 0 ended, when the last ended
+    out.append({"workload": "stage-trace", "part": "start", "start_spread_us": round(u[:, 0].max(), 2),
+                "embedding_median_us": round(float(np.median(u[:, 1])), 2), "embedding_max_us": round(u[:, 1].max(), 2),
+                "layer0_end_us": round(u[:, 2 + 5].max(), 2), "last_end_us": round(u[:, 2 + 6 * L].max(), 2)})
     for k in range(6):
         out.append({"workload": "stage-trace", "stage": names[k], "us_slowest_workgroup": round(dur[k] / n, 2),
                     "end_median_us": round(med[k] / n, 2), "end_skew_us": round(skew[k] / n, 2)})
