@@ -91,7 +91,7 @@ typedef struct lkhip_profile {
     uint64_t lm_head_launches;
     double lm_head_ms;         /* the single largest matvec, lm_head */
     double lm_head_bytes;
-    double attn_ms;            /* flash-decoding partial + merge */
+    double attn_ms;            /* flash-decoding attention: one launch per layer, partials folded in-kernel */
     double other_ms;           /* norms, rope, gather, argmax */
 } lkhip_profile;
 
@@ -155,8 +155,11 @@ int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t kv_type, l
 void lkhip_session_destroy(lkhip_session* s);
 /* Session::forward (src/engine.rs:51): one token at pos -> vocab logits (host). */
 int lkhip_session_forward(lkhip_session* s, uint32_t token, size_t pos, float* logits_out);
-/* Session::prefill (src/engine.rs:56-62): the token loop; logits of the last
- * position into logits_out (may be NULL). */
+/* Session::prefill (src/engine.rs:56-62): the chunked multi-row pass (up to
+ * 512 positions per pass, each linear layer one GEMM reading its weights once),
+ * within 1e-3 of lokal's token loop; LKHIP_PREFILL=loop runs the token loop
+ * instead (bit-identical to forward).  Logits of the last position into
+ * logits_out (may be NULL). */
 int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size_t n, float* logits_out);
 /* Session::forward_batch (src/engine.rs:67-70): logits for every position,
  * n * vocab floats. */
@@ -167,8 +170,13 @@ int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids, size_t n,
  * host round trip per token.  logits_last (may be NULL) gets the final logits. */
 int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, size_t pos, size_t n_steps, uint32_t* ids_out,
                                 float* logits_last);
-/* Read back the f16 KV cache row of one layer at pos as f32 (kv_dim values). */
+/* Read back one layer's KV cache row at pos as f32 (kv_dim values), from the
+ * session's f16 or f32 cache (lkhip_session_create_ex's kv_type). */
 int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int which_v, float* out);
+/* Rows pos0..pos0+n-1 of the same cache, out[n][kv_dim] as f32.  A read-back
+ * for tests and debugging, as read_kv; lokal's KvCache exposes its buffers the
+ * same way (src/model.rs:114-128). */
+int lkhip_session_read_kv_rows(lkhip_session* s, uint32_t layer, size_t pos0, size_t n, int which_v, float* out);
 /* Kernel timing: on != 0 brackets every launch with hipEvents (eager launches,
  * no graph) until switched off; profile_get sums since the last reset. */
 int lkhip_session_set_profiling(lkhip_session* s, int on);
@@ -201,6 +209,11 @@ int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, size_t n_rows
  * the device; ids_out is n_steps * n_rows ids, step-major.  n_rows <= 64. */
 int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, size_t n_rows, size_t n_steps,
                               uint32_t* ids_out);
+/* Rows pos0..pos0+n-1 of one slot's f16 KV cache at one layer, out[n][kv_dim]
+ * as f32: a read-back of MetalBatcher's per-slot pool for tests
+ * (src/gpu/metal.rs:3557-3565). */
+int lkhip_batch_read_kv_rows(lkhip_batch* b, uint32_t slot, uint32_t layer, size_t pos0, size_t n, int which_v,
+                             float* out);
 
 /* ------------------------------------------------------------ memory */
 

@@ -156,6 +156,14 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
 // writeback is needed.  Wave w folds heads w, w+4: lane k holds chunk k's
 // (m, l), and every lane its dim of all chunks' acc -- one round trip for
 // the lot (nch <= LK_MAXCH = 64).
+// Memory order of the arrival count.  Acquire-release at agent scope makes the
+// fold's visibility a guarantee of the memory model rather than of the
+// write-through partial stores; LK_ATTN_FOLD_ORDER=__ATOMIC_RELAXED builds the
+// variant that relies on the stores alone (kept for measurement).
+#ifndef LK_ATTN_FOLD_ORDER
+#define LK_ATTN_FOLD_ORDER __ATOMIC_ACQ_REL
+#endif
+
 template <int G>
 __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t nch) {
     __shared__ uint32_t last;
@@ -165,7 +173,7 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
     __syncthreads();
     if (tid == 0) {
         uint32_t* cnt = a.cnt + ((size_t)seq * a.n_kv + kvh) * LK_ATTN_CNT_STRIDE;
-        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+        last = __hip_atomic_fetch_add(cnt, 1u, LK_ATTN_FOLD_ORDER, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
     }
     __syncthreads();
     if (!last) return;

@@ -553,7 +553,7 @@ struct lkhip_session {
     int kv_f32 = 0;
     DevBuf x, xn, qkv, att, inner, logits, part, keys, head_epoch, err, state, feed, ids_out;
     LkStepState* h_state = nullptr;  // pinned
-    float* h_logits = nullptr;       // pinned
+    float* h_logits = nullptr;       // pinned; max(vocab, max_seq) words: logits or greedy ids
     uint32_t head_blocks = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -856,7 +856,9 @@ extern "C" int lkhip_session_create_ex(lkhip_engine* e, size_t max_seq, uint32_t
         if (rp) s->fused_rep = std::min<uint32_t>(LK_FUSED_REP, std::max<uint32_t>(1, (uint32_t)atoi(rp)));
     }
     HIP_OR_FAIL(hipHostMalloc((void**)&s->h_state, sizeof(LkStepState), hipHostMallocDefault));
-    HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
+    // The staging buffer carries either one row of logits or up to max_seq greedy ids.
+    HIP_OR_FAIL(hipHostMalloc((void**)&s->h_logits, std::max<size_t>(c.vocab_size, max_seq) * 4,
+                              hipHostMallocDefault));
     if (want_graph(s.get()) && (rc = build_graph(s.get()))) return rc;
     *out = s.release();
     return LKHIP_OK;
@@ -999,37 +1001,63 @@ extern "C" int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, siz
     return LKHIP_OK;
 }
 
-extern "C" int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int which_v, float* out) {
-    if (!s || !out) return fail(LKHIP_E_INVALID, "read_kv: null argument");
-    const lkhip_config& c = s->e->cfg;
-    if (layer >= c.num_hidden_layers || pos >= s->max_seq) return fail(LKHIP_E_INVALID, "read_kv: out of range");
-    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
-    const size_t el = s->kv_f32 ? 4 : 2;
-    const uint8_t* base = (which_v ? s->vc : s->kc).as<uint8_t>() + (size_t)layer * kv_layer_elems(s) * el;
-    std::vector<uint8_t> h(64 * el);
-    for (uint32_t kh = 0; kh < c.num_key_value_heads; kh++) {
-        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * s->kv_seq + pos) * 64 * el, 64 * el,
-                              hipMemcpyDeviceToHost));
-        if (s->kv_f32) {
-            memcpy(&out[kh * 64], h.data(), 256);
-            continue;
+static float half_bits_to_f32(uint16_t hb16) {
+    uint32_t hb = hb16, sign = (hb >> 15) << 31, ex = (hb >> 10) & 31, m = hb & 1023, bits;
+    if (ex == 0) {
+        if (m == 0) bits = sign;
+        else {
+            int k = -1;
+            do { m <<= 1; k++; } while (!(m & 1024));
+            bits = sign | ((uint32_t)(112 - k) << 23) | ((m & 1023) << 13);
         }
-        for (int d = 0; d < 64; d++) {
-            const uint16_t hb16 = (uint16_t)(h[2 * d] | (h[2 * d + 1] << 8));
-            uint32_t hb = hb16, sign = (hb >> 15) << 31, ex = (hb >> 10) & 31, m = hb & 1023, bits;
-            if (ex == 0) {
-                if (m == 0) bits = sign;
-                else {
-                    int k = -1;
-                    do { m <<= 1; k++; } while (!(m & 1024));
-                    bits = sign | ((uint32_t)(112 - k) << 23) | ((m & 1023) << 13);
-                }
-            } else if (ex == 31) bits = sign | 0x7f800000u | (m << 13);
-            else bits = sign | ((ex + 112) << 23) | (m << 13);
-            memcpy(&out[kh * 64 + d], &bits, 4);
+    } else if (ex == 31) bits = sign | 0x7f800000u | (m << 13);
+    else bits = sign | ((ex + 112) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Rows pos0..pos0+n-1 of one layer's cache, laid out [kv_head][kv_seq][64]
+// from `base`, into out[n][n_kv * 64] as f32.
+static int read_kv_rows(const uint8_t* base, uint32_t n_kv, size_t kv_seq, bool f32, size_t pos0, size_t n,
+                        float* out) {
+    const size_t el = f32 ? 4 : 2;
+    std::vector<uint8_t> h(n * 64 * el);
+    for (uint32_t kh = 0; kh < n_kv; kh++) {
+        HIP_OR_FAIL(hipMemcpy(h.data(), base + ((size_t)kh * kv_seq + pos0) * 64 * el, n * 64 * el,
+                              hipMemcpyDeviceToHost));
+        for (size_t r = 0; r < n; r++) {
+            float* o = out + r * n_kv * 64 + kh * 64;
+            if (f32) {
+                memcpy(o, h.data() + r * 256, 256);
+                continue;
+            }
+            for (int d = 0; d < 64; d++) {
+                const uint8_t* b = h.data() + (r * 64 + d) * 2;
+                o[d] = half_bits_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            }
         }
     }
     return LKHIP_OK;
+}
+
+extern "C" int lkhip_session_read_kv_rows(lkhip_session* s, uint32_t layer, size_t pos0, size_t n, int which_v,
+                                          float* out) {
+    if (!s || (!out && n)) return fail(LKHIP_E_INVALID, "read_kv: null argument");
+    const lkhip_config& c = s->e->cfg;
+    if (layer >= c.num_hidden_layers || pos0 > s->max_seq || n > s->max_seq - pos0)
+        return fail(LKHIP_E_INVALID, "read_kv: out of range");
+    if (n == 0) return LKHIP_OK;
+    HIP_OR_FAIL(hipStreamSynchronize(s->stream));
+    const size_t el = s->kv_f32 ? 4 : 2;
+    const uint8_t* base = (which_v ? s->vc : s->kc).as<uint8_t>() + (size_t)layer * kv_layer_elems(s) * el;
+    return read_kv_rows(base, c.num_key_value_heads, s->kv_seq, s->kv_f32 != 0, pos0, n, out);
+}
+
+extern "C" int lkhip_session_read_kv(lkhip_session* s, uint32_t layer, size_t pos, int which_v, float* out) {
+    if (!s || !out) return fail(LKHIP_E_INVALID, "read_kv: null argument");
+    if (pos >= s->max_seq) return fail(LKHIP_E_INVALID, "read_kv: out of range");
+    return lkhip_session_read_kv_rows(s, layer, pos, 1, which_v, out);
 }
 
 extern "C" int lkhip_session_set_profiling(lkhip_session* s, int on) {
@@ -1342,8 +1370,15 @@ static int rows_prefill(const lkhip_engine* e, Rows& R, const KvDesc& kv, uint32
         int rc = rows_upload(R, ids + off, pos.data(), slots.data(), m, st);
         if (rc) return rc;
         const bool last = off + m == n;
-        hipError_t err = enqueue_rows(e, R, m, kv, last && logits_out ? HEAD_LAST : HEAD_NONE, st);
-        if (err != hipSuccess) return fail(LKHIP_E_HIP, "batched prefill launch failed: %s", hipGetErrorString(err));
+        // Through the gate: a long prefill on this stream must not hold CUs while
+        // another stream's one-kernel step needs every workgroup resident.
+        rc = gated_launch(e->device, st, [&]() -> int {
+            hipError_t err = enqueue_rows(e, R, m, kv, last && logits_out ? HEAD_LAST : HEAD_NONE, st);
+            if (err != hipSuccess)
+                return fail(LKHIP_E_HIP, "batched prefill launch failed: %s", hipGetErrorString(err));
+            return LKHIP_OK;
+        });
+        if (rc) return rc;
     }
     if (logits_out)
         HIP_OR_FAIL(hipMemcpyAsync(logits_out, R.logits.p, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, st));
@@ -1430,8 +1465,12 @@ extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids
         const uint32_t m = (uint32_t)std::min<size_t>(chunk, n - off);
         for (uint32_t i = 0; i < m; i++) pos[i] = pos0 + off + i;
         if ((rc = rows_upload(R, ids + off, pos.data(), slots.data(), m, s->stream))) return rc;
-        hipError_t err = enqueue_rows(s->e, R, m, kv, HEAD_ALL, s->stream);
-        if (err != hipSuccess) return fail(LKHIP_E_HIP, "forward_batch launch failed: %s", hipGetErrorString(err));
+        rc = gated_launch(s->e->device, s->stream, [&]() -> int {
+            hipError_t err = enqueue_rows(s->e, R, m, kv, HEAD_ALL, s->stream);
+            if (err != hipSuccess) return fail(LKHIP_E_HIP, "forward_batch launch failed: %s", hipGetErrorString(err));
+            return LKHIP_OK;
+        });
+        if (rc) return rc;
         HIP_OR_FAIL(hipMemcpyAsync(logits_out + off * V, R.logits.p, m * V * 4, hipMemcpyDeviceToHost, s->stream));
     }
     HIP_OR_FAIL(hipStreamSynchronize(s->stream));
@@ -1837,6 +1876,19 @@ extern "C" int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, 
         if ((rc = batch_enqueue_step(b, n, true, fused))) return rc;
     HIP_OR_FAIL(hipMemcpyAsync(ids_out, b->rows.out_ids.p, need * 4, hipMemcpyDeviceToHost, b->stream));
     return batch_sync_check(b, fused);
+}
+
+extern "C" int lkhip_batch_read_kv_rows(lkhip_batch* b, uint32_t slot, uint32_t layer, size_t pos0, size_t n,
+                                        int which_v, float* out) {
+    if (!b || (!out && n)) return fail(LKHIP_E_INVALID, "read_kv: null argument");
+    const lkhip_config& c = b->e->cfg;
+    if (slot >= b->n_slots || layer >= c.num_hidden_layers || pos0 > b->max_seq || n > b->max_seq - pos0)
+        return fail(LKHIP_E_INVALID, "read_kv: out of range");
+    if (n == 0) return LKHIP_OK;
+    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
+    const uint8_t* base = (which_v ? b->kv.vc : b->kv.kc) + (size_t)layer * b->kv.layer_bytes +
+                          (size_t)slot * b->kv.slot_elems * 2;
+    return read_kv_rows(base, c.num_key_value_heads, b->kv.kv_seq, false, pos0, n, out);
 }
 
 // ------------------------------------------------------------------ memory

@@ -124,12 +124,14 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // gridDim / LK_XCDS workgroups: the CP hands workgroups to the XCDs in
     // turn, so each XCD holds the same number of them, and an arrival counter
     // per XCD numbers them (counters only grow: slot = count mod the XCD's
-    // share).
+    // share).  The counter wraps at the share (atomic increment modulo nslot),
+    // so it never passes 2^32 and hands out duplicate slots there when nslot
+    // is not a power of two.
     const uint32_t xcd = __builtin_amdgcn_s_getreg(LK_HWREG_XCC_ID) & (LK_XCDS - 1);
     const uint32_t nslot = gridDim.x / LK_XCDS;
     if (threadIdx.x == 0)
-        *slot_lds = __hip_atomic_fetch_add(a.xcd_cnt + xcd * LK_XCD_CNT_STRIDE, 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT) % nslot;
+        *slot_lds = __builtin_amdgcn_atomic_inc32(a.xcd_cnt + xcd * LK_XCD_CNT_STRIDE, nslot - 1,
+                                                  __ATOMIC_RELAXED, "agent") % nslot;
     {
         const uint32_t* src = (const uint32_t*)a.layers;
         uint32_t* dst = (uint32_t*)lay;

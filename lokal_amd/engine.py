@@ -181,6 +181,12 @@ class Session:
         check(lib().lkhip_session_read_kv(self._h, layer, pos, int(which_v), _f32p(out)))
         return out
 
+    def read_kv_rows(self, layer: int, pos0: int, n: int, which_v: bool) -> np.ndarray:
+        """Cache rows pos0..pos0+n-1 of one layer, [n][kv_dim] f32."""
+        out = np.empty((n, self.engine.cfg.kv_dim()), dtype=np.float32)
+        check(lib().lkhip_session_read_kv_rows(self._h, layer, pos0, n, int(which_v), _f32p(out)))
+        return out
+
     def set_profiling(self, on: bool) -> None:
         check(lib().lkhip_session_set_profiling(self._h, int(on)))
 
@@ -251,6 +257,12 @@ class Batcher:
         arr = (Row * len(rows))(*[Row(r.token, r.slot, r.pos) for r in rows])
         out = np.empty((n_steps, len(rows)), dtype=np.uint32)
         check(lib().lkhip_batch_decode_greedy(self._h, arr, len(rows), n_steps, _u32p(out)))
+        return out
+
+    def read_kv_rows(self, slot: int, layer: int, pos0: int, n: int, which_v: bool) -> np.ndarray:
+        """One slot's cache rows pos0..pos0+n-1 of one layer, [n][kv_dim] f32."""
+        out = np.empty((n, self.engine.cfg.kv_dim()), dtype=np.float32)
+        check(lib().lkhip_batch_read_kv_rows(self._h, slot, layer, pos0, n, int(which_v), _f32p(out)))
         return out
 
     def close(self):

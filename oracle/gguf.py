@@ -15,9 +15,12 @@ lokal_amd/csrc/gguf.hip).  Restates, in Python over the file's bytes:
     files carry q/k rows in the converter's RoPE order, undone at load.
 The tensors come back as raw bytes under HF names with the llama flag; the
 oracle Model dequantizes them and undoes the permutation itself
-(oracle_unpermute_llama_qk, src/gguf/arch.rs:274-286).  Only the checks the
-parity tests need are restated: the reader's refusals are tested against the
-product directly (tests/test_gguf.py).
+(oracle_unpermute_llama_qk, src/gguf/arch.rs:274-286).  The container walk
+(read_container) is pinned on the reference's own tiny_gguf fixture and its
+asserted facts (src/gguf/testutil.rs:9-42, container.rs:474-513); of the
+reader's refusals it restates the ones those tests assert (bad magic,
+big-endian, version, truncation); the rest are tested against the product
+directly (tests/test_gguf.py).
 """
 from __future__ import annotations
 
@@ -79,13 +82,20 @@ def hf_name(g: str) -> str | None:
     return f"model.layers.{int(idx)}.{m}.{kind}"
 
 
-def read_gguf(path) -> tuple[ModelConfig, list[Tensor], bool]:
-    """(config, tensors under HF names with the file's raw bytes, llama_permuted)."""
-    b = Path(path).read_bytes()
+def read_container(src) -> tuple[int, dict, list[tuple[str, tuple[int, ...], int, np.ndarray]]]:
+    """GgufFile::open (src/gguf/container.rs:161-288) over a path or the
+    file's bytes: (version, kv, [(name, dims row-major, ggml type, data
+    bytes)]).  Raises ValueError with the reference's reasons for a bad magic,
+    a big-endian file, a version other than 2/3, a header that ends early and
+    a tensor whose data runs past the file."""
+    b = bytes(src) if isinstance(src, (bytes, bytearray, memoryview)) else Path(src).read_bytes()
     rd = _Rd(b)
     if rd.take(4) != b"GGUF":
-        raise ValueError("bad magic")
+        raise ValueError("not a GGUF file (bad magic)")
     version = rd.unpack("<I")
+    swapped = int.from_bytes(version.to_bytes(4, "little"), "big")
+    if swapped in (2, 3):
+        raise ValueError("big-endian GGUF files are not supported")
     if version not in (2, 3):
         raise ValueError(f"GGUF version {version} unsupported")
     n_tensors, n_kv = rd.unpack("<Q"), rd.unpack("<Q")
@@ -102,7 +112,20 @@ def read_gguf(path) -> tuple[ModelConfig, list[Tensor], bool]:
         infos.append((name, ne, ty, off))
     align = int(kv.get("general.alignment", 32))
     data_start = (rd.p + align - 1) // align * align
+    out = []
+    for name, ne, ty, off in infos:
+        nb = row_bytes(ty, int(np.prod(ne)))
+        start = data_start + off
+        if start + nb > len(b):
+            raise ValueError(f"tensor {name}: {nb} bytes at data offset {off} run past the file")
+        data = np.frombuffer(b, dtype=np.uint8, count=nb, offset=start).copy()
+        out.append((name, tuple(reversed(ne)), ty, data))  # fastest-first -> row-major
+    return version, kv, out
 
+
+def read_gguf(path) -> tuple[ModelConfig, list[Tensor], bool]:
+    """(config, tensors under HF names with the file's raw bytes, llama_permuted)."""
+    _, kv, raw = read_container(path)
     arch = kv["general.architecture"]
     k = lambda s: kv[f"{arch}.{s}"]  # noqa: E731
     heads, hidden = int(k("attention.head_count")), int(k("embedding_length"))
@@ -115,13 +138,9 @@ def read_gguf(path) -> tuple[ModelConfig, list[Tensor], bool]:
                       max_position_embeddings=int(kv.get(f"{arch}.context_length", 4096)),
                       head_dim=int(kv.get(f"{arch}.attention.key_length", 0)))
     tensors = []
-    for name, ne, ty, off in infos:
+    for name, dims, ty, data in raw:
         hf = hf_name(name)
         if hf is None:
             continue
-        n = int(np.prod(ne))
-        start = data_start + off
-        nb = row_bytes(ty, n)
-        data = np.frombuffer(b, dtype=np.uint8, count=nb, offset=start).copy()
-        tensors.append(Tensor(hf, ty, tuple(reversed(ne)), data))
+        tensors.append(Tensor(hf, ty, dims, data))
     return cfg, tensors, arch == "llama"

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle.gguf import read_gguf
+from oracle.gguf import read_container, read_gguf
 from tests.gguf_writer import write_gguf
 from lokal_amd import Engine, LokalHipError, gguf_config, synth
 from lokal_amd.config import ModelConfig
@@ -75,6 +75,42 @@ def test_reference_tiny_fixture_parses_then_asks_for_the_config(tmp_path, align)
     p.write_bytes(_tiny_fixture(3, align))
     with pytest.raises(LokalHipError, match="llama.embedding_length is missing"):
         gguf_config(p)
+
+
+@pytest.mark.parametrize("version,align", [(3, None), (2, 64), (3, 16)])
+def test_oracle_reads_the_reference_tiny_fixture_as_gguffile_open_does(version, align):
+    """The oracle's container walk on the reference's tiny_gguf bytes
+    (src/gguf/testutil.rs:9-42) gives what the reference's own tests assert
+    of GgufFile::open (src/gguf/container.rs:474-494): the version, one
+    tensor, the architecture string, dims [2, 32] (ne reversed to row-major),
+    type Q8_0 and 68 data bytes at the alignment boundary."""
+    b = _tiny_fixture(version, align)
+    v, kv, tensors = read_container(b)
+    assert v == version and len(tensors) == 1
+    assert kv["general.architecture"] == "llama"
+    if align is not None:
+        assert kv["general.alignment"] == align
+    name, dims, ty, data = tensors[0]
+    assert (name, dims, ty, data.size) == ("t", (2, 32), 8, 68)
+    # the data section starts at the first alignment boundary after the header
+    a = align or 32
+    assert len(b) - 68 == -(-(len(b) - 68) // a) * a and not data.any()
+
+
+def test_oracle_refuses_what_the_reference_tests_refuse():
+    """container.rs:496-513: a big-endian version word and a file cut 40 bytes
+    short; plus the bad magic and version checks of GgufFile::open."""
+    b = bytearray(_tiny_fixture(3, None))
+    be = bytearray(b)
+    be[4:8] = struct.pack(">I", 3)
+    with pytest.raises(ValueError, match="big-endian"):
+        read_container(be)
+    with pytest.raises(ValueError, match="truncated|run past"):
+        read_container(b[:-40])
+    with pytest.raises(ValueError, match="bad magic"):
+        read_container(b"GGML" + bytes(b[4:]))
+    with pytest.raises(ValueError, match="version 1 unsupported"):
+        read_container(_tiny_fixture(1, None))
 
 
 def test_refusals(tmp_path):

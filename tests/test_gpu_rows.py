@@ -386,3 +386,78 @@ def test_batcher_graph_replay_matches_direct_launches(batch_path, monkeypatch):
     assert np.array_equal(runs["1"][1], runs["0"][1])
     eng.close()
     om.close()
+
+
+def _batcher_against_oracle_on_its_cache(kind, max_seq, lens, plan, seed):
+    """Prefill each slot through the Batcher, hand the oracle every slot's f16
+    cache rows, then run the steps of `plan` (lists of slots stepped
+    together): every row's logits must match the oracle continuing from the
+    same cache, within the f16 bar (the current row's own K/V is rounded by
+    each side), and after each step the oracle takes the row the GPU wrote."""
+    cfg, eng, om = build(kind, seed=seed)
+    rng = np.random.default_rng(seed)
+    bat = eng.batcher(len(lens), max_seq)
+    orc = []
+    L = cfg.num_hidden_layers
+    for slot, n in enumerate(lens):
+        bat.prefill(slot, rng.integers(0, cfg.vocab_size, n).astype(np.uint32))
+        o = om.session(max_seq, kv_f16=True)
+        for layer in range(L):
+            for which_v in (False, True):
+                o.load_kv(layer, 0, which_v, bat.read_kv_rows(slot, layer, 0, n, which_v))
+        orc.append(o)
+    print(f"{kind} max_seq {max_seq}: {len(lens)} slots prefilled, caches loaded", flush=True)
+    pos = list(lens)
+    worst = 0.0
+    for step, slots in enumerate(plan):
+        rows = [BatchRow(int(rng.integers(0, cfg.vocab_size)), pos[s], s) for s in slots]
+        outs = bat.decode_step(rows)
+        for r, out in zip(rows, outs):
+            e = rel_err(out, orc[r.slot].forward(r.token, r.pos))
+            worst = max(worst, e)
+            assert e < TOL_F16_KV, (step, r.slot, r.pos, e)
+            for layer in range(L):
+                for which_v in (False, True):
+                    orc[r.slot].load_kv(layer, r.pos, which_v, bat.read_kv_rows(r.slot, layer, r.pos, 1, which_v))
+            pos[r.slot] += 1
+    print(f"{kind} max_seq {max_seq}: {len(plan)} steps, worst logits rel err {worst:.3g}, last positions {pos}")
+    for o in orc:
+        o.close()
+    bat.close()
+    eng.close()
+    om.close()
+    return pos
+
+
+@pytest.mark.parametrize("kind", ["q8_0", "f16"])
+def test_batcher_rows_near_4096_positions_across_the_path_switch(kind):
+    """A Batcher whose cache holds 4096 positions runs 2-row steps on the
+    multi-row one-kernel step up to position 4095 (its attention stage takes
+    64 tiles per row there), 3-row steps on the per-layer launches (too many
+    attention items for one grid) and 1-row steps on the single-row kernel,
+    interleaved on the same slots up to the cache's last position."""
+    plan = [[0, 1], [0, 1, 2], [2], [1, 2], [0, 1, 2, 3], [3], [0, 3]] * 3
+    lens = [4060, 4070, 4050, 4000]
+    pos = _batcher_against_oracle_on_its_cache(kind, 4096, lens, plan, seed=40)
+    assert max(pos) <= 4096
+
+
+@pytest.mark.parametrize("kind", ["q8_0", "f16"])
+def test_batcher_rows_from_4000_to_4200_positions(kind):
+    """A Batcher past the multi-row kernel's 4096-position cache runs its
+    multi-row steps as per-layer launches and 1-row steps on the single-row
+    kernel: rows cross position 4096 (the 65th 64-position tile) in both."""
+    plan = [[0, 1, 2]] * 6 + [[0]] * 3 + [[1, 2]] * 4 + [[2]] * 2
+    lens = [4090, 4093, 4095]
+    pos = _batcher_against_oracle_on_its_cache(kind, 4200, lens, plan, seed=41)
+    assert min(pos) > 4096
+
+
+def test_batcher_four_rows_at_16k_positions():
+    """BASELINE config 5's batched decode shape: 4 concurrent sequences with
+    independent contexts near 16384 positions, one query token each per step
+    (4-row steps), then single-row steps (the one-kernel step with 64 chunks
+    of 4 tiles per head)."""
+    plan = [[0, 1, 2, 3]] * 4 + [[1]] * 2 + [[0, 1, 2, 3]] * 2
+    lens = [16300, 16000, 16200, 16100]
+    _batcher_against_oracle_on_its_cache("q8_0", 16384, lens, plan, seed=42)
