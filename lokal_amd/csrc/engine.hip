@@ -613,7 +613,7 @@ static LkMvArgs mv_args(const float* x, uint32_t cols) {
 }
 
 // Final RMSNorm + lm_head + argmax + step advance (lmhead.hip).
-static hipError_t enqueue_head(lkhip_session* s, const float* x, uint32_t x_stride, hipStream_t st) {
+static LkHeadArgs head_args(lkhip_session* s, const float* x, uint32_t x_stride, bool defer) {
     const lkhip_engine* e = s->e;
     LkHeadArgs a{};
     a.x = x;
@@ -630,7 +630,24 @@ static hipError_t enqueue_head(lkhip_session* s, const float* x, uint32_t x_stri
     a.st = s->state.as<LkStepState>();
     a.feed = s->feed.as<uint32_t>();
     a.ids_out = s->ids_out.as<uint32_t>();
-    return lk_lm_head_launch(a, s->head_blocks, st);
+    a.defer = defer ? 1u : 0u;
+    return a;
+}
+// Whether the one-kernel step path defers the lm_head's argmax fold to the
+// next step's start (LKHIP_HEAD_DEFER=0: the lm_head's block 0 collects the
+// keys itself, as on the per-stage path).
+static bool head_deferred() {
+    const char* d = getenv("LKHIP_HEAD_DEFER");
+    return !(d && d[0] == '0');
+}
+// defer: the one-kernel step path, whose next step (or head_finish) folds the keys
+static hipError_t enqueue_head(lkhip_session* s, const float* x, uint32_t x_stride, bool defer, hipStream_t st) {
+    return lk_lm_head_launch(head_args(s, x, x_stride, defer), s->head_blocks, st);
+}
+// Folds a deferred lm_head's keys into the step state, if still pending: after
+// the last step of a device-side loop, so the state and ids are final.
+static hipError_t enqueue_head_finish(lkhip_session* s, hipStream_t st) {
+    return lk_head_finish_launch(head_args(s, nullptr, 1, true), s->head_blocks, st);
 }
 
 // The whole decode step of one token (Model::forward, src/model.rs:196-262)
@@ -670,6 +687,11 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
         a.max_seq = (uint32_t)s->kv_seq;
         a.max_chunks = s->max_chunks;
         a.st = state;
+        a.head_keys = head_deferred() ? s->keys.as<uint64_t>() : nullptr;
+        a.head_blocks = s->head_blocks;
+        a.head_epoch = s->head_epoch.as<uint32_t>();
+        a.feed = s->feed.as<uint32_t>();
+        a.ids_out = s->ids_out.as<uint32_t>();
         a.epoch = s->epoch.as<uint32_t>();
         a.err = s->err.as<uint32_t>();
         a.xcd_cnt = s->xcd_cnt.as<uint32_t>();
@@ -689,7 +711,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
              C_MATVEC, e->matvec_bytes - e->lm_head->bytes);
         // the last layer's output: f32 halves of the (f32 | epoch) words
         STEP(enqueue_head(s, (const float*)(s->xb.as<uint64_t>() + (size_t)(c.num_hidden_layers & 1) * LK_FUSED_REP * h),
-                          2, st),
+                          2, head_deferred(), st),
              C_LMHEAD, e->lm_head->bytes);
         return hipSuccess;
     }
@@ -770,7 +792,7 @@ static hipError_t enqueue_step(lkhip_session* s, Rec& rec) {
             STEP(lk_matvec_launch(a, LK_MV_ACC, st), C_MATVEC, ly.down->bytes);
         }
     }
-    STEP(enqueue_head(s, x, 1, st), C_LMHEAD, e->lm_head->bytes);
+    STEP(enqueue_head(s, x, 1, false, st), C_LMHEAD, e->lm_head->bytes);
 #undef STEP
     return hipSuccess;
 }
@@ -927,6 +949,16 @@ static int run_step(lkhip_session* s) {
     return LKHIP_OK;
 }
 
+// After a run of steps: the one-kernel path leaves the last lm_head's keys
+// pending (the next step would fold them); fold them now so the state and
+// the ids are final.
+static int finish_steps(lkhip_session* s) {
+    if (!s->use_fused || !head_deferred()) return LKHIP_OK;
+    hipError_t err = enqueue_head_finish(s, s->stream);
+    if (err != hipSuccess) return fail(LKHIP_E_HIP, "decode step finish launch failed: %s", hipGetErrorString(err));
+    return LKHIP_OK;
+}
+
 static int check_tok(lkhip_session* s, uint32_t token, size_t pos) {
     if (token >= s->e->cfg.vocab_size)
         return fail(LKHIP_E_INVALID, "token id %u is outside the vocabulary (%u)", token, s->e->cfg.vocab_size);
@@ -944,8 +976,9 @@ static int sync_check(lkhip_session* s) {
     if (!flag) return LKHIP_OK;
     HIP_OR_FAIL(hipMemset(s->err.p, 0, 4));
     if (!(flag & 1)) {
-        return fail(LKHIP_E_HIP, "the lm_head launch timed out collecting its workgroups' argmax keys (is every CU "
-                                 "free?) — the token and state of that step are invalid; restart from a known position");
+        return fail(LKHIP_E_HIP, "the lm_head's argmax keys were incomplete when folded (a collection timed out: is "
+                                 "every CU free?) — the token and state of that step are invalid; restart from a known "
+                                 "position");
     }
     // bit 0: a wait inside the one-kernel step timed out (bit 1 may be set too)
     s->use_fused = false;
@@ -994,6 +1027,7 @@ extern "C" int lkhip_session_decode_greedy(lkhip_session* s, uint32_t token, siz
     if ((rc = set_state(s, token, pos, 0))) return rc;
     for (size_t i = 0; i < n_steps; i++)
         if ((rc = run_step(s))) return rc;
+    if ((rc = finish_steps(s))) return rc;
     HIP_OR_FAIL(hipMemcpyAsync(s->h_logits, s->ids_out.p, n_steps * 4, hipMemcpyDeviceToHost, s->stream));
     if ((rc = sync_check(s))) return rc;
     memcpy(ids_out, s->h_logits, n_steps * 4);
@@ -1433,6 +1467,7 @@ extern "C" int lkhip_session_prefill(lkhip_session* s, const uint32_t* ids, size
     if ((rc = set_state(s, ids[0], 0, (uint32_t)(n - 1)))) return rc;
     for (size_t i = 0; i < n; i++)
         if ((rc = run_step(s))) return rc;
+    if ((rc = finish_steps(s))) return rc;
     if (logits_out) return copy_logits(s, logits_out);
     return sync_check(s);
 }

@@ -25,6 +25,17 @@ struct LkFusedArgs {
     uint64_t kv_layer;   // elements per layer of one cache
     uint32_t max_seq, max_chunks;
     LkStepState* st;
+    // the session's deferred lm_head (lmhead.hip, LkHeadArgs::defer): when
+    // st->pending, every workgroup folds the head_blocks argmax keys (epoch
+    // *head_epoch + 1) into the step state at its start; block 0 writes the
+    // advanced state back at the end (pending again: this step's lm_head
+    // follows), the argmax to ids_out, and advances *head_epoch.  Null
+    // head_keys: no fold (a Batcher row, meta set).
+    const uint64_t* head_keys;
+    uint32_t head_blocks;
+    uint32_t* head_epoch;
+    const uint32_t* feed;
+    uint32_t* ids_out;
     uint32_t* epoch;     // token counter of the exchange epochs
     uint32_t* err;       // set when a bounded wait timed out
     uint32_t* xcd_cnt;   // fused.hip: per-XCD arrival counters (LK_XCDS words, LK_XCD_CNT_STRIDE apart), zeroed

@@ -148,14 +148,88 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // Batcher row, meta set) row 0 of the Batcher's row table, whose cache
     // slot selects the KV rows
     uint32_t pos, token, slot = 0;
+    // the session's step state (and, for block 0, what it writes back at the end)
+    // (kept in LDS until block 0 writes it back at the end: held in registers
+    // across the layers it would spill, and a spill reload waits for every
+    // weight row in flight)
+    __shared__ uint32_t st_keep[9];
+    uint32_t n_out = 0, n_feed = 0, fed = 0, best_id = 0, out_at = 0;
+    bool folded = false, took_argmax = false;
     if (a.meta) {
         token = __builtin_amdgcn_readfirstlane(a.meta[0]);
         pos = __builtin_amdgcn_readfirstlane(a.meta[a.meta_cap]);
         slot = __builtin_amdgcn_readfirstlane(a.meta[2 * a.meta_cap]);
     } else {
-        const LkStepState st = *a.st;
-        pos = st.pos;
-        token = st.token;
+        // the state, the key epoch and this thread's key words are loaded
+        // together (the keys whether or not they turn out to be pending), so
+        // the fold costs one memory round trip before the embedding row
+        const uint4 s0 = *(const uint4*)lk_g((const uint32_t*)a.st);
+        const uint2 s1 = *(const uint2*)lk_g((const uint32_t*)a.st + 4);  // fed, pending
+        static_assert(LK_HEAD_MAX_BLOCKS <= 2 * FT, "two lm_head blocks' keys per thread");
+        uint64_t kw[4] = {0, 0, 0, 0};
+        uint32_t hep = 0;  // the epoch of the keys to fold
+        if (a.head_keys) {
+            hep = *lk_g(a.head_epoch) + 1;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t i = threadIdx.x + (uint32_t)(k >> 1) * FT;
+                if (i < a.head_blocks)
+                    kw[k] = __hip_atomic_load(a.head_keys + 2 * i + (k & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        token = s0.x;
+        pos = s0.y;
+        n_out = s0.z;
+        n_feed = s0.w;
+        fed = s1.x;
+        if (s1.y && a.head_keys) {
+            // The previous step's lm_head left its per-block argmax keys:
+            // fold them here, where the token is consumed (every workgroup
+            // does, from the same words), and advance the step as the greedy
+            // loop does.  wv (per-wave LDS) is free until the layers start.
+            uint64_t* kb = (uint64_t*)(wv);
+            bool ok = true;
+            uint64_t b = 0;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const uint32_t i = threadIdx.x + (uint32_t)k * FT;
+                if (i < a.head_blocks) {
+                    ok &= (uint32_t)(kw[2 * k] >> 32) == hep && (uint32_t)(kw[2 * k + 1] >> 32) == hep;
+                    const uint64_t kk = (kw[2 * k] << 32) | (kw[2 * k + 1] & 0xFFFFFFFFu);
+                    b = kk > b ? kk : b;
+                }
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                const uint64_t o = __shfl_xor(b, m, 64);
+                b = o > b ? o : b;
+            }
+            if (lane == 0) kb[wave] = b;
+            if (!ok) (void)__hip_atomic_fetch_or(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lds_barrier();
+            b = kb[0];
+#pragma unroll
+            for (int w2 = 1; w2 < FW; w2++) b = kb[w2] > b ? kb[w2] : b;
+            best_id = lk_argmax_idx(b);
+            took_argmax = n_feed == 0;
+            out_at = n_out;
+            lk_step_advance(token, pos, n_out, n_feed, fed, best_id, a.feed, nullptr, false);
+            folded = true;
+            lds_barrier();  // kb is reused as wave scratch below
+        }
+        token = __builtin_amdgcn_readfirstlane(token);
+        pos = __builtin_amdgcn_readfirstlane(pos);
+        if (threadIdx.x == 0) {
+            st_keep[0] = token;
+            st_keep[1] = pos;
+            st_keep[2] = n_out;
+            st_keep[3] = n_feed;
+            st_keep[4] = fed;
+            st_keep[5] = (folded ? 1u : 0u) | (took_argmax ? 2u : 0u);
+            st_keep[6] = best_id;
+            st_keep[7] = out_at;
+            st_keep[8] = hep;
+        }
     }
     KV* const kc0 = (KV*)a.kc + (size_t)slot * a.slot_elems;
     KV* const vc0 = (KV*)a.vc + (size_t)slot * a.slot_elems;
@@ -723,7 +797,22 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // The final RMSNorm, lm_head and argmax run in the next launch
     // (lmhead.hip); every block has read `base`, so the epoch may advance.
     LKF_MARK(2 + 6 * nL);
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.epoch[0] = base + 1;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.epoch[0] = base + 1;
+        if (!a.meta && a.head_keys) {
+            // every block has read the state: write this step's back, pending
+            // the lm_head launch that follows
+            const uint32_t fl = st_keep[5];
+            if (fl & 1) {
+                if (a.ids_out && (fl & 2)) a.ids_out[st_keep[7]] = st_keep[6];
+                *a.head_epoch = st_keep[8];  // the folded launch's epoch
+            }
+            uint32_t* sp = (uint32_t*)a.st;
+            *(uint4*)sp = make_uint4(st_keep[0], st_keep[1], st_keep[2], st_keep[3]);
+            sp[4] = st_keep[4];
+            sp[5] = 1;
+        }
+    }
     if (tracing && threadIdx.x == 0)
         for (uint32_t k = 0; k < lk_fused_trace_len(nL); k++) a.trace[(size_t)blockIdx.x * lk_fused_trace_len(nL) + k] = ltr[k];
 }

@@ -147,8 +147,49 @@ struct LkStepState {
     uint32_t n_out;   // argmax ids written so far
     uint32_t n_feed;  // prompt ids still to feed before argmax takes over
     uint32_t fed;     // prompt ids fed so far
-    uint32_t pad[3];
+    // 1 when the last step's lm_head launch published its per-block argmax
+    // keys without folding them (LkHeadArgs::defer): the state above is that
+    // step's, and whoever reads it next (the one-kernel step's start, or
+    // lk_head_finish) folds the keys and advances it first
+    uint32_t pending;
+    uint32_t pad[2];
 };
+static_assert(sizeof(LkStepState) == 32, "read as two 16-byte words");
+
+// The lm_head's per-block argmax keys (lk_argmax_key), each published as two
+// words (epoch | high half) and (epoch | low half): a word carrying the
+// launch's epoch is that launch's, so the buffer never needs clearing.
+// Thread t of nt folds blocks t, t + nt, ... of n; ok turns false if a word
+// does not carry ep (read after the launch ended, every word must).
+__device__ __forceinline__ uint64_t lk_head_keys_fold(const uint64_t* keys, uint32_t n, uint32_t ep, uint32_t t,
+                                                      uint32_t nt, bool& ok) {
+    uint64_t best = 0;
+    for (uint32_t i = t; i < n; i += nt) {
+        const uint64_t hi = __hip_atomic_load(keys + 2 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t lo = __hip_atomic_load(keys + 2 * i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok &= (uint32_t)(hi >> 32) == ep && (uint32_t)(lo >> 32) == ep;
+        const uint64_t k = (hi << 32) | (lo & 0xFFFFFFFFu);
+        best = k > best ? k : best;
+    }
+    return best;
+}
+// The greedy loop's step advance (src/generate.rs:101-118 at -t 0): feed the
+// next prompt id while any are left, else take the argmax (writing it to
+// ids_out, if given); the position moves on by one.
+__device__ __forceinline__ void lk_step_advance(uint32_t& token, uint32_t& pos, uint32_t& n_out, uint32_t& n_feed,
+                                                uint32_t& fed, uint32_t best, const uint32_t* feed,
+                                                uint32_t* ids_out, bool write_id) {
+    if (n_feed > 0) {
+        token = feed[fed];
+        fed += 1;
+        n_feed -= 1;
+    } else {
+        if (ids_out && write_id) ids_out[n_out] = best;
+        n_out += 1;
+        token = best;
+    }
+    pos += 1;
+}
 hipError_t lk_embed_step_launch(const LkDevW& table, const LkStepState* st_dev, float* x, hipStream_t st);
 hipError_t lk_rope_kv_launch(float* qkv, uint32_t n_heads, uint32_t n_kv, const LkFreq& freq,
                              const LkStepState* st_dev, const uint32_t* pos_rows, uint32_t n_rows,
@@ -174,12 +215,21 @@ struct LkHeadArgs {
     LkStepState* st;
     const uint32_t* feed;
     uint32_t* ids_out;
+    // 1: every block publishes its key and the launch ends there; the state
+    // is left pending (the one-kernel step that follows folds the keys, or
+    // lk_head_finish does).  0: block 0 collects the keys and advances the
+    // state itself.
+    uint32_t defer;
 };
 // lm_head rows of up to 256 16-byte chunks (Q8_0: h <= 4096, F16: 2048, Q4_K: 8192)
 bool lk_lm_head_fits(uint32_t type, uint32_t h);
 uint32_t lk_lm_head_rows(uint32_t type, uint32_t h);
 uint32_t lk_lm_head_blocks(uint32_t vocab, uint32_t type, uint32_t h);
 hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t st);
+// Folds the keys of a deferred lm_head launch of `blocks` blocks into the
+// state (if it is pending) and advances the key epoch: the end of a run of
+// one-kernel steps.  One small launch.
+hipError_t lk_head_finish_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t st);
 
 // Attention (attention.hip).  q rows of n_heads*64, caches f16
 // [seq][n_kv][max_seq][64]; ctx from ctx_len[seq] or, when null, st_dev->pos+1.
