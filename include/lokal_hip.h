@@ -214,6 +214,15 @@ int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, size_t n_ro
  * (src/gpu/metal.rs:3557-3565). */
 int lkhip_batch_read_kv_rows(lkhip_batch* b, uint32_t slot, uint32_t layer, size_t pos0, size_t n, int which_v,
                              float* out);
+/* Phase timeline of the last persistent multi-row step (the Batcher's
+ * one-launch step for several rows): s_memrealtime ticks (100 MHz) of its
+ * first workgroup at the start and after each grid barrier (the embedding,
+ * then q/k/v, attention, o_proj, gate/up, down of every layer).  Recorded
+ * only when LKHIP_BSTEP_TRACE=1 was set when the batcher was created; the
+ * counterpart of lkhip_session_trace, for the per-phase times of
+ * LOKAL_GPU_TIMING's table (src/gpu/metal.rs:3856-3952). */
+size_t lkhip_batch_trace_len(const lkhip_batch* b);
+int lkhip_batch_trace(lkhip_batch* b, uint64_t* ticks, size_t n);
 
 /* ------------------------------------------------------------ memory */
 

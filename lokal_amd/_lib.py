@@ -84,6 +84,8 @@ SIGNATURES = {
     "lkhip_session_read_kv": (C.c_int, [_P, C.c_uint32, C.c_size_t, C.c_int, _F]),
     "lkhip_session_read_kv_rows": (C.c_int, [_P, C.c_uint32, C.c_size_t, C.c_size_t, C.c_int, _F]),
     "lkhip_batch_read_kv_rows": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_size_t, C.c_size_t, C.c_int, _F]),
+    "lkhip_batch_trace_len": (C.c_size_t, [_P]),
+    "lkhip_batch_trace": (C.c_int, [_P, C.POINTER(C.c_uint64), C.c_size_t]),
     "lkhip_session_set_profiling": (C.c_int, [_P, C.c_int]),
     "lkhip_session_profile": (C.c_int, [_P, C.POINTER(Profile), C.c_int]),
     "lkhip_session_set_trace": (C.c_int, [_P, C.c_int]),

@@ -19,6 +19,7 @@
 #include "../../include/lokal_hip.h"
 #include "lkhip_common.h"
 #include "fused.h"
+#include "batch_step.h"
 #include "gguf.h"
 #include "repack.h"
 
@@ -333,6 +334,10 @@ static int fused_setup(lkhip_engine* e) {
     int cus = 0;
     HIP_OR_FAIL(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
     e->fused_blocks = (unsigned)cus;
+    if (const char* fb = getenv("LKHIP_FUSED_BLOCKS")) {  // measurement: fewer workgroups than CUs
+        const int v = atoi(fb);
+        if (v > 0 && v <= cus) e->fused_blocks = (unsigned)v;
+    }
     const uint32_t nw = e->fused_blocks * (uint32_t)(lk_fused_threads() / 64);
     if ((c.num_attention_heads + 2 * c.num_key_value_heads) * 32 > nw || h > nw) {
         e->fused_why = "more rows per stage than waves";
@@ -1539,11 +1544,16 @@ struct lkhip_batch {
     uint32_t single_chunks = 0;
     DevBuf sxb, sqb, spb, sab, sxpb, sib, sepoch, sxcd;
     std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
+    // the persistent multi-row step (batch_step.hip) for bstep_min..64 rows
+    bool bstep_ok = false;
+    uint32_t bstep_min = 0;
+    DevBuf bs_ss, bs_part, bs_cnt, bs_bar, bs_epoch, bs_trace;
+    std::vector<hipGraphExec_t> bstep_graph[2];  // [greedy] by row count
     void drop_fused_graphs() {
-        for (auto& v : fused_graph) {
-            for (auto g : v)
+        for (auto* vv : {&fused_graph[0], &fused_graph[1], &bstep_graph[0], &bstep_graph[1]}) {
+            for (auto g : *vv)
                 if (g) (void)hipGraphExecDestroy(g);
-            v.clear();
+            vv->clear();
         }
     }
     ~lkhip_batch() {
@@ -1657,6 +1667,120 @@ static hipError_t batch_enqueue_single(lkhip_batch* b, hipStream_t st) {
                            b->single_lds, st, false);
 }
 
+// Fewest rows a step takes on the persistent multi-row step by default: none
+// (LK_BS_MAX_ROWS + 1).  Measured on MI355X at the Qwen2.5-0.5B Q8_0 shape it
+// is slower than the paths it would replace at every row count (2 rows 1.54
+// ms per step against 0.59 on fused_rows_kernel, 16 rows 1.70 against 1.55 on
+// the per-layer launches, 64 rows 2.64 against 2.32): its five grid barriers
+// and split-K round trips per layer cost ~9 us a phase before any work.
+// LKHIP_BATCH_STEP_MIN=n turns it on from n rows.
+#ifndef LK_BSTEP_MIN_ROWS
+#define LK_BSTEP_MIN_ROWS (LK_BS_MAX_ROWS + 1)
+#endif
+// Shapes the persistent multi-row step takes: one weight type across the
+// layers (fused_setup checked it), an instantiated GQA group, hidden and
+// intermediate widths in whole 32-column blocks (Q4_K: 256), q/k/v segments in
+// whole 16-row tiles, at most LK_BS_MAXT 128-column tiles of hidden.
+static bool bstep_shape_ok(const lkhip_engine* e) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t wt = e->layers[0].q->dw.type, G = (uint32_t)e->fused_g;
+    if (wt != LKHIP_Q8_0 && wt != LKHIP_F16 && wt != LKHIP_Q4_K) return false;
+    if (G != 3 && G != 4 && G != 7 && G != 8) return false;
+    const uint32_t blk = wt == LKHIP_Q4_K ? 256 : 32;
+    if (c.hidden_size % blk || c.intermediate_size % blk || e->qd % blk) return false;
+    if (c.hidden_size > 128 * LK_BS_MAXT || c.num_hidden_layers > 50) return false;
+    return e->qd % 16 == 0 && e->kvd % 16 == 0;
+}
+
+// Split-K plan of the persistent multi-row step's linear layers for n rows:
+// enough (output tile, K split) items for every CU, each split at least one
+// 128-column chunk.
+struct BsPlan {
+    uint32_t ks[4], per[4];
+    size_t part_floats;
+};
+static BsPlan bstep_plan(const lkhip_engine* e, uint32_t n) {
+    const lkhip_config& c = e->cfg;
+    const uint32_t h = c.hidden_size, I = c.intermediate_size, qd = e->qd, kvd = e->kvd;
+    const uint32_t NK[4][3] = {{qd + 2 * kvd, h, 1}, {h, qd, 1}, {I, h, 2}, {h, I, 1}};  // N, K, outputs
+    BsPlan p{};
+    const uint32_t rb = 16 * lk_batch_step_mb(n), bt = (n + rb - 1) / rb;
+    for (int g = 0; g < 4; g++) {
+        const uint32_t nt = (NK[g][0] + 127) / 128, nck = (NK[g][1] + 127) / 128;
+        // the split whose busiest workgroup runs the fewest chunks (items per
+        // workgroup x chunks per item); a tie goes to fewer splits
+        uint32_t best = ~0u;
+        for (uint32_t ks = 1; ks <= nck; ks++) {
+            const uint32_t per = (nck + ks - 1) / ks, ks2 = (nck + per - 1) / per;
+            const uint32_t rounds = (nt * bt * ks2 + e->fused_blocks - 1) / e->fused_blocks;
+            const uint32_t cost = rounds * per;
+            if (cost < best) {
+                best = cost;
+                p.per[g] = per;
+                p.ks[g] = ks2;
+            }
+        }
+        if (p.ks[g] > 1)
+            p.part_floats = std::max<size_t>(p.part_floats, (size_t)p.ks[g] * n * NK[g][0] * NK[g][2]);
+    }
+    return p;
+}
+
+// The persistent multi-row step over the rows whose meta is on the device,
+// leaving the final x rows in rows.x.
+static hipError_t batch_enqueue_bstep(lkhip_batch* b, uint32_t n, hipStream_t st) {
+    const lkhip_engine* e = b->e;
+    const lkhip_config& c = e->cfg;
+    Rows& R = b->rows;
+    LkBatchStepArgs a{};
+    a.layers = e->fused_layers.as<LkFusedLayer>();
+    a.n_layers = c.num_hidden_layers;
+    a.embed = e->embed->dw;
+    a.freq = e->freq;
+    a.h = c.hidden_size;
+    a.I = c.intermediate_size;
+    a.nh = c.num_attention_heads;
+    a.nkv = c.num_key_value_heads;
+    a.eps = c.rms_norm_eps;
+    a.meta = R.meta.as<uint32_t>();
+    a.meta_cap = R.cap;
+    a.nrows = n;
+    a.kc = b->kv.kc;
+    a.vc = b->kv.vc;
+    a.layer_bytes = b->kv.layer_bytes;
+    a.slot_elems = b->kv.slot_elems;
+    a.kv_seq = b->kv.kv_seq;
+    a.x = R.x.as<float>();
+    a.ss = b->bs_ss.as<float>();
+    a.qkv = R.qkv.as<float>();
+    a.att = R.att.as<float>();
+    a.inner = R.inner.as<float>();
+    a.part = b->bs_part.as<float>();
+    a.cnt = b->bs_cnt.as<uint32_t>();
+    const BsPlan p = bstep_plan(e, n);
+    for (int g = 0; g < 4; g++) {
+        a.ks[g] = p.ks[g];
+        a.per[g] = p.per[g];
+    }
+    LkAttnArgs& at = a.attn;
+    at.ctx_len = a.meta + 3 * R.cap;
+    at.slots = a.meta + 2 * R.cap;
+    at.n_seq = n;
+    at.n_heads = c.num_attention_heads;
+    at.n_kv = c.num_key_value_heads;
+    at.max_seq = b->kv.kv_seq;
+    at.seq_stride = b->kv.slot_elems;
+    at.q_stride = e->qd + 2 * e->kvd;
+    at.kv_f32 = 0;
+    lk_attn_bind_scratch(at, R.apart.as<float>(), (size_t)R.cap * c.num_key_value_heads);
+    (void)lk_attn_set_plan(at);
+    a.bar = b->bs_bar.as<uint64_t>();
+    a.epoch = b->bs_epoch.as<uint32_t>();
+    a.err = b->ferr.as<uint32_t>();
+    a.trace = b->bs_trace.p ? b->bs_trace.as<uint64_t>() : nullptr;
+    return lk_batch_step_launch(a, e->layers[0].q->dw.type, e->fused_g, e->fused_blocks, st, false);
+}
+
 // Whether the one-kernel step takes rows at these positions (the largest of
 // each row over the call): one wave per (row, head, 64-position tile).
 static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
@@ -1672,16 +1796,32 @@ static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& la
     return items <= (size_t)b->e->fused_blocks * (lk_fused_threads() / 64);
 }
 
+// The device path of a step of these rows: 2 the persistent multi-row step
+// (bstep_min rows and up), 1 the one-kernel steps (one row, or a few rows
+// that fit fused_rows_kernel), 0 the per-layer launches.
+enum { PATH_LAYERS = 0, PATH_FUSED = 1, PATH_BSTEP = 2 };
+static int batch_path(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
+    const size_t n = last_pos.size();
+    if (n == 1 && b->single_ok) return PATH_FUSED;
+    if (b->bstep_ok && n >= b->bstep_min && n <= LK_BS_MAX_ROWS) return PATH_BSTEP;
+    return batch_fused_fits(b, last_pos) ? PATH_FUSED : PATH_LAYERS;
+}
+
 // Enqueues a decode step of n rows (meta on the device); greedy adds the
 // argmax feedback.  Replays a captured graph when graphs are on.  fused: the
 // multi-row one-kernel step instead of the per-layer launches.
-static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, bool fused = false) {
+static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, int path = PATH_LAYERS) {
     std::vector<hipGraphExec_t>& cache =
-        fused ? b->fused_graph[greedy ? 1 : 0] : (greedy ? b->greedy_graph : b->step_graph);
+        path == PATH_BSTEP ? b->bstep_graph[greedy ? 1 : 0]
+                           : (path == PATH_FUSED ? b->fused_graph[greedy ? 1 : 0]
+                                                 : (greedy ? b->greedy_graph : b->step_graph));
     auto body = [&](hipStream_t st) -> hipError_t {
-        hipError_t err = !fused ? enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st)
-                                : (n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st));
-        if (err == hipSuccess && fused) err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
+        hipError_t err;
+        if (path == PATH_BSTEP) err = batch_enqueue_bstep(b, n, st);
+        else if (path == PATH_FUSED) err = n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st);
+        else err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        if (err == hipSuccess && path != PATH_LAYERS)
+            err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;
         return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
                                       b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
@@ -1794,6 +1934,32 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         HIP_OR_FAIL(hipMemcpy(b->sepoch.p, &one, 4, hipMemcpyHostToDevice));
         b->single_ok = true;
     }
+    // the persistent multi-row step (LKHIP_BATCH_STEP=0 leaves it off;
+    // LKHIP_BATCH_STEP_MIN sets the fewest rows it takes)
+    const char* bse = getenv("LKHIP_BATCH_STEP");
+    if (e->fused_ok && !(bse && bse[0] == '0') && !(fe && fe[0] == '0') && bstep_shape_ok(e)) {
+        LkBatchStepArgs probe{};
+        if (lk_batch_step_launch(probe, e->layers[0].q->dw.type, e->fused_g, e->fused_blocks, nullptr, true) ==
+            hipSuccess) {
+            size_t part = 0;
+            for (uint32_t n = 2; n <= LK_BS_MAX_ROWS; n++) part = std::max(part, bstep_plan(e, n).part_floats);
+            if ((rc = dev_alloc(b->bs_ss, (size_t)LK_BS_MAX_ROWS * LK_BS_MAXT * 4)) ||
+                (rc = dev_alloc(b->bs_part, std::max<size_t>(part, 1) * 4)) ||
+                (rc = dev_alloc(b->bs_cnt, (size_t)4 * LK_BS_CNT_PER_GEMM * LK_ATTN_CNT_STRIDE * 4)) ||
+                (rc = dev_alloc(b->bs_bar, (size_t)e->fused_blocks * 8)) || (rc = dev_alloc(b->bs_epoch, 4)))
+                return rc;
+            if (!b->ferr.p && (rc = dev_alloc(b->ferr, 4))) return rc;
+            const char* bt = getenv("LKHIP_BSTEP_TRACE");
+            if (bt && bt[0] == '1' &&
+                (rc = dev_alloc(b->bs_trace, (size_t)lk_batch_step_trace_len(c.num_hidden_layers) * 8)))
+                return rc;
+            const char* bm = getenv("LKHIP_BATCH_STEP_MIN");
+            b->bstep_min = bm ? (uint32_t)std::max(2, atoi(bm)) : (uint32_t)LK_BSTEP_MIN_ROWS;
+            b->bstep_ok = true;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
     *out = b.release();
     return LKHIP_OK;
 }
@@ -1810,6 +1976,7 @@ static int batch_sync_check(lkhip_batch* b, bool fused) {
     HIP_OR_FAIL(hipMemset(b->ferr.p, 0, 4));
     b->fused_ok = false;
     b->single_ok = false;
+    b->bstep_ok = false;
     b->drop_fused_graphs();
     return fail(LKHIP_E_HIP, "the batcher's one-kernel step timed out waiting on another workgroup (is every CU "
                              "free?) — this batcher now runs the per-layer kernels; repeat the call");
@@ -1868,9 +2035,9 @@ extern "C" int lkhip_batch_decode_step(lkhip_batch* b, const lkhip_row* rows, si
         const uint32_t m = (uint32_t)std::min<size_t>(LK_ROWS_LOGITS, n_rows - off);
         std::vector<size_t> last(m);
         for (uint32_t i = 0; i < m; i++) last[i] = (size_t)rows[off + i].pos;
-        const bool fused = batch_fused_fits(b, last);
-        any_fused |= fused;
-        if ((rc = batch_upload_rows(b, rows + off, m)) || (rc = batch_enqueue_step(b, m, false, fused))) return rc;
+        const int path = batch_path(b, last);
+        any_fused |= path != PATH_LAYERS;
+        if ((rc = batch_upload_rows(b, rows + off, m)) || (rc = batch_enqueue_step(b, m, false, path))) return rc;
         HIP_OR_FAIL(hipMemcpyAsync(logits_out + off * V, b->rows.logits.p, m * V * 4, hipMemcpyDeviceToHost, b->stream));
     }
     return batch_sync_check(b, any_fused);
@@ -1894,23 +2061,36 @@ extern "C" int lkhip_batch_decode_greedy(lkhip_batch* b, const lkhip_row* rows, 
                 (void)hipGraphExecDestroy(g);
                 g = nullptr;
             }
-        for (auto& g : b->fused_graph[1])
-            if (g) {
-                (void)hipGraphExecDestroy(g);
-                g = nullptr;
-            }
+        for (auto* vv : {&b->fused_graph[1], &b->bstep_graph[1]})
+            for (auto& g : *vv)
+                if (g) {
+                    (void)hipGraphExecDestroy(g);
+                    g = nullptr;
+                }
         b->rows.out_ids = DevBuf();
         if ((rc = dev_alloc(b->rows.out_ids, need * 4))) return rc;
         b->rows.out_ids_cap = need;
     }
     std::vector<size_t> last(n);
     for (uint32_t i = 0; i < n; i++) last[i] = (size_t)rows[i].pos + n_steps - 1;
-    const bool fused = batch_fused_fits(b, last);
+    const int path = batch_path(b, last);
     if ((rc = batch_upload_rows(b, rows, n))) return rc;
     for (size_t s = 0; s < n_steps; s++)
-        if ((rc = batch_enqueue_step(b, n, true, fused))) return rc;
+        if ((rc = batch_enqueue_step(b, n, true, path))) return rc;
     HIP_OR_FAIL(hipMemcpyAsync(ids_out, b->rows.out_ids.p, need * 4, hipMemcpyDeviceToHost, b->stream));
-    return batch_sync_check(b, fused);
+    return batch_sync_check(b, path != PATH_LAYERS);
+}
+
+extern "C" size_t lkhip_batch_trace_len(const lkhip_batch* b) {
+    return b && b->bs_trace.p ? lk_batch_step_trace_len(b->e->cfg.num_hidden_layers) : 0;
+}
+extern "C" int lkhip_batch_trace(lkhip_batch* b, uint64_t* ticks, size_t n) {
+    if (!b || (!ticks && n)) return fail(LKHIP_E_INVALID, "batch trace: null argument");
+    const size_t len = lkhip_batch_trace_len(b);
+    if (!len) return fail(LKHIP_E_UNSUPPORTED, "batch trace: set LKHIP_BSTEP_TRACE=1 before creating the batcher");
+    HIP_OR_FAIL(hipStreamSynchronize(b->stream));
+    HIP_OR_FAIL(hipMemcpy(ticks, b->bs_trace.p, std::min(n, len) * 8, hipMemcpyDeviceToHost));
+    return LKHIP_OK;
 }
 
 extern "C" int lkhip_batch_read_kv_rows(lkhip_batch* b, uint32_t slot, uint32_t layer, size_t pos0, size_t n,

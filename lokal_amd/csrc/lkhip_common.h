@@ -250,6 +250,9 @@ struct LkAttnArgs {
     uint32_t waves, tiles, cstride;  // set by lk_attn_launch: its chunk plan and partial slots per head
 };
 uint32_t lk_attn_chunk(uint32_t max_seq);
+// Sets a's chunk plan (waves, tiles, cstride) for its n_seq, n_kv and
+// max_seq, as lk_attn_launch does; returns the chunks per (sequence, kv head).
+uint32_t lk_attn_set_plan(LkAttnArgs& a);
 size_t lk_attn_part_floats(uint32_t n_seq, uint32_t n_heads, uint32_t max_seq);
 // A launch's scratch buffer: a region of cnt_cap arrival counters (u32,
 // one per (sequence, kv head), n_seq * n_kv <= cnt_cap) that must be zero

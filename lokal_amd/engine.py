@@ -259,6 +259,14 @@ class Batcher:
         check(lib().lkhip_batch_decode_greedy(self._h, arr, len(rows), n_steps, _u32p(out)))
         return out
 
+    def trace_ticks(self) -> np.ndarray:
+        """Phase timestamps (100 MHz) of the last persistent multi-row step:
+        start, after the embedding, then 5 per layer (LKHIP_BSTEP_TRACE=1)."""
+        n = int(lib().lkhip_batch_trace_len(self._h))
+        t = np.zeros(max(n, 1), dtype=np.uint64)
+        check(lib().lkhip_batch_trace(self._h, t.ctypes.data_as(C.POINTER(C.c_uint64)), n))
+        return t
+
     def read_kv_rows(self, slot: int, layer: int, pos0: int, n: int, which_v: bool) -> np.ndarray:
         """One slot's cache rows pos0..pos0+n-1 of one layer, [n][kv_dim] f32."""
         out = np.empty((n, self.engine.cfg.kv_dim()), dtype=np.float32)

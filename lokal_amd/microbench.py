@@ -354,7 +354,9 @@ def batch() -> list[dict]:
     rng = np.random.default_rng(12)
     out = []
     steps = 64
-    for B in (1, 2, 3, 4, 8, 16, 64):
+    import os
+    rows_list = [int(v) for v in os.environ.get("LKHIP_MB_ROWS", "1,2,3,4,8,16,32,64").split(",")]
+    for B in rows_list:
         bat = eng.batcher(B, 512 + steps + 16)
         first = []
         for slot in range(B):

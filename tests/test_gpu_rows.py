@@ -173,14 +173,21 @@ def test_forward_batch_matches_oracle_per_position(kind):
     om.close()
 
 
-# The Batcher's two device paths: the multi-row one-kernel step (fused_rows.hip,
-# up to 4 rows, where the model's shape has one) and the per-layer launches.
-BATCH_PATHS = ["fused", "layers"]
+# The Batcher's three device paths: the persistent multi-row step
+# (batch_step.hip, "bstep"), the multi-row one-kernel step (fused_rows.hip, up
+# to 8 rows, "fused") and the per-layer launches ("layers").
+BATCH_PATHS = ["bstep", "fused", "layers"]
+
+
+def set_batch_path(monkeypatch, path):
+    monkeypatch.setenv("LKHIP_BATCH_FUSED", "0" if path == "layers" else "1")
+    monkeypatch.setenv("LKHIP_BATCH_STEP", "1" if path == "bstep" else "0")
+    monkeypatch.setenv("LKHIP_BATCH_STEP_MIN", "2")
 
 
 @pytest.fixture
 def batch_path(request, monkeypatch):
-    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1" if request.param == "fused" else "0")
+    set_batch_path(monkeypatch, request.param)
     return request.param
 
 
@@ -279,7 +286,7 @@ def test_batcher_fused_step_every_row_count(kind, n_rows, monkeypatch):
     2-8 rows: the 2-, 4- and 8-row kernels, fewer rows padded), on slots
     other than 0..n-1: every row against the oracle over steps that cross a
     64-position tile, then greedy ids against the oracle's."""
-    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
+    set_batch_path(monkeypatch, "fused")
     cfg, eng, om = build(kind, seed=10 + n_rows)
     rng = np.random.default_rng(n_rows)
     lens = [60, 3, 127, 64, 1, 100, 20, 63][:n_rows]
@@ -319,7 +326,7 @@ def test_batcher_one_row_steps_mixed_with_multi_row_steps_and_a_session(kind, mo
     multi-row steps on the same slots and with a Session of the same engine
     stepping in between, and every row stays equal to the oracle's own
     sequence (src/engine.rs:42-47)."""
-    monkeypatch.setenv("LKHIP_BATCH_FUSED", "1")
+    set_batch_path(monkeypatch, "fused")
     cfg, eng, om = build(kind, seed=21)
     rng = np.random.default_rng(21)
     lens = [70, 2, 33]
@@ -461,3 +468,55 @@ def test_batcher_four_rows_at_16k_positions():
     plan = [[0, 1, 2, 3]] * 4 + [[1]] * 2 + [[0, 1, 2, 3]] * 2
     lens = [16300, 16000, 16200, 16100]
     _batcher_against_oracle_on_its_cache("q8_0", 16384, lens, plan, seed=42)
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n_rows", [2, 9, 16, 33, 64])
+def test_batcher_persistent_step_every_row_band(kind, n_rows, monkeypatch):
+    """The persistent multi-row step (one launch per step, grid barriers
+    between its phases) at 2-64 rows on slots in scrambled order, rows at
+    different positions: every row's logits against the oracle's own
+    sequence over three steps (crossing a 64-position tile for some rows),
+    then 8 greedy steps on the device against a per-step host loop."""
+    set_batch_path(monkeypatch, "bstep")
+    cfg, eng, om = build(kind, seed=60 + n_rows)
+    rng = np.random.default_rng(60 + n_rows)
+    lens = [int(rng.integers(1, 140)) for _ in range(n_rows)]
+    lens[0] = 63
+    slots = list(rng.permutation(64)[:n_rows])
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    bat = eng.batcher(64, 192)
+    orc = [om.session(192, kv_f16=True) for _ in lens]
+    for i, p in enumerate(prompts):
+        bat.prefill(int(slots[i]), p)
+        orc[i].prefill(p)
+    pos = list(lens)
+    worst = 0.0
+    for step in range(3):
+        toks = [int(rng.integers(0, cfg.vocab_size)) for _ in lens]
+        outs = bat.decode_step([BatchRow(toks[i], pos[i], int(slots[i])) for i in range(n_rows)])
+        for i in range(n_rows):
+            e = rel_err(outs[i], orc[i].forward(toks[i], pos[i]))
+            worst = max(worst, e)
+            assert e < TOL_F16_KV, (step, i, e)
+            pos[i] += 1
+    print(f"{kind} rows={n_rows}: worst logits rel err {worst:.3g}")
+    first = [int(rng.integers(0, cfg.vocab_size)) for _ in lens]
+    ids = bat.decode_greedy([BatchRow(first[i], pos[i], int(slots[i])) for i in range(n_rows)], 8)
+    assert ids.shape == (8, n_rows)
+    short = 0
+    for i in range(n_rows):
+        t, agree = first[i], 8
+        for k in range(8):
+            t = int(oracle.argmax(orc[i].forward(t, pos[i] + k)))
+            if t != ids[k, i]:
+                agree = k
+                break
+        short += agree < 8
+        assert agree >= 4, (i, agree)
+    print(f"{kind} rows={n_rows}: {n_rows - short}/{n_rows} rows with 8/8 greedy ids equal to the CPU path's")
+    bat.close()
+    for o in orc:
+        o.close()
+    eng.close()
+    om.close()
