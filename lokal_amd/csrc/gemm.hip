@@ -29,6 +29,9 @@
 // sums them in a fixed order and runs the epilogue.
 #include "gemm_impl.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace lkg {
 
 // Epilogue of one output element: segment n (global index over segments).
@@ -196,6 +199,254 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same GEMM at the f16 matrix-core rate (v_mfma_f32_16x16x32_f16) with
+// f32-level accuracy, for Q8_0 and F16 weights:
+//   X      each row of a 128-column chunk is scaled by a power of two s (its
+//          largest |x| brought into [0.5, 1)) and split into f16 hi + lo
+//          (x/s = hi + lo to ~22 significant bits; the scaling is exact),
+//          staged in LDS as two f16 planes;
+//   W      one MFMA covers exactly one 32-column Q8_0 block: lane (j, m) holds
+//          weights 8j..8j+7 of the block of row m (int8 -> f16 exactly: the
+//          byte biased by 128 is the low mantissa byte of 1024 + q + 128, a
+//          packed subtraction removes the bias); F16 weights as they are;
+//   sums   D = W (hi + lo) per block in f32, then y_chunk += d * D with the
+//          block's scale d (Q8_0), and y += s * y_chunk per chunk.
+// The products q * (hi or lo) are exact in f32, so the result differs from
+// the f32 kernel's only by the split's ~2^-22 and the summation order.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t HS = KC + 8;  // LDS row stride of an f16 plane (halves)
+
+template <int WT> struct Raw16;
+template <> struct Raw16<LK_Q8_0> { uint2 q[4]; uint32_t d; };
+template <> struct Raw16<LK_F16> { uint4 q[4]; };
+
+// Lane (j, m = row r) of chunk c: weights 8j..8j+7 of each of the chunk's four
+// 32-column blocks of row r; Q8_0 also the scale of row r, block 4c + j.
+template <int WT>
+__device__ __forceinline__ void raw16_load(Raw16<WT>& R, const LkDevW& w, uint32_t r, uint32_t c, uint32_t j,
+                                           uint32_t K) {
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+        uint32_t col = c * KC + 32 * blk + 8 * j;
+        col = col < K ? col : 0;  // past K: any in-row weights, multiplied by X = 0
+        if constexpr (WT == LK_Q8_0) R.q[blk] = *(const uint2*)(w.data + (size_t)r * w.cols + col);
+        else R.q[blk] = *(const uint4*)(w.data + ((size_t)r * w.cols + col) * 2);
+    }
+    if constexpr (WT == LK_Q8_0) {
+        const uint32_t b = c * 4 + j;
+        R.d = ((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + (b < K / 32 ? b : 0)];
+    }
+}
+
+// 8 weights of block blk as f16.
+template <int WT>
+__device__ __forceinline__ h8 raw16_w(const Raw16<WT>& R, int blk) {
+    if constexpr (WT == LK_F16) {
+        return __builtin_bit_cast(h8, R.q[blk]);
+    } else {
+        const hh2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const uint32_t w0 = R.q[blk].x ^ 0x80808080u, w1 = R.q[blk].y ^ 0x80808080u;
+        // bytes [u, 0x64, u', 0x64]: the f16 value 1024 + u (u = q + 128)
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+        const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+        const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+        const hh2 q0 = __builtin_bit_cast(hh2, p0) - bias, q1 = __builtin_bit_cast(hh2, p1) - bias;
+        const hh2 q2 = __builtin_bit_cast(hh2, p2) - bias, q3 = __builtin_bit_cast(hh2, p3) - bias;
+        return h8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+    }
+}
+
+template <int WT, int MB, int MODE>
+__global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
+    constexpr bool SW = MODE == LK_MV_SWIGLU;
+    constexpr int BR = 16 * MB;
+    constexpr int NW = SW ? 2 : 1;
+    __shared__ __align__(16) _Float16 xh[2][BR * HS], xl[2][BR * HS];
+    __shared__ float xsc[2][BR];
+    __shared__ __align__(16) float sd[4][NW][64];  // per wave: the chunk's block scales, [block][row]
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t n0 = (blockIdx.x * 4 + wave) * 16;
+    const bool live = n0 < a.N;
+    const uint32_t B = a.n_rows, K = a.K;
+    const uint32_t b0 = blockIdx.y * BR;
+    const uint32_t nck = (K + KC - 1) / KC;
+    const uint32_t per = (nck + a.ks - 1) / a.ks;
+    const uint32_t c_begin = blockIdx.z * per;
+    const uint32_t c_end = c_begin + per < nck ? c_begin + per : nck;
+    const uint32_t j = (uint32_t)lane >> 4;
+
+    uint32_t si = 0, nb = 0;
+    if constexpr (!SW) {
+        while (si + 1 < a.nseg && n0 >= nb + a.seg[si].w.rows) {
+            nb += a.seg[si].w.rows;
+            si++;
+        }
+    }
+    const LkDevW W0 = a.seg[si].w;
+    const LkDevW W1 = a.seg[SW ? 1 : si].w;
+    uint32_t r = live ? n0 - nb + ((uint32_t)lane & 15) : 0;
+    r = r < W0.rows ? r : W0.rows - 1;
+
+    // X staging: thread t takes float4 number t + 256 i of the BR x KC tile; the
+    // 32 threads of a row are 32 adjacent lanes (the row's scale by shuffles)
+    constexpr int XV = BR * KC / 4 / 256;
+    float4 xv[XV];
+    auto x_fetch = [&](uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            uint32_t bb = b0 + row;
+            bb = bb < B ? bb : B - 1;
+            const uint32_t k = c * KC + col;
+            xv[i] = k < K ? *(const float4*)(a.x + (size_t)bb * a.ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto x_store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            float mx = fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w)));
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            int ex = 0;
+            (void)frexpf(mx, &ex);                       // mx = f * 2^ex, f in [0.5, 1) (ex = 0 for 0)
+            const float inv = ldexpf(1.0f, -ex), sc = ldexpf(1.0f, ex);
+            const float v[4] = {xv[i].x * inv, xv[i].y * inv, xv[i].z * inv, xv[i].w * inv};  // exact
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                hi[q] = (_Float16)v[q];
+                lo[q] = (_Float16)(v[q] - (float)hi[q]);
+            }
+            *(uint2*)&xh[buf][row * HS + col] = __builtin_bit_cast(uint2, hi);
+            *(uint2*)&xl[buf][row * HS + col] = __builtin_bit_cast(uint2, lo);
+            if (col == 0) xsc[buf][row] = sc;
+        }
+    };
+
+    f4 y[MB], yu[SW ? MB : 1];
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        y[m] = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (SW) yu[m] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    Raw16<WT> cur, nxt, curu, nxtu;
+    if (c_begin < c_end) {
+        x_fetch(c_begin);
+        x_store(0);
+        if (live) {
+            raw16_load(cur, W0, r, c_begin, j, K);
+            if constexpr (SW) raw16_load(curu, W1, r, c_begin, j, K);
+        }
+    }
+    for (uint32_t c = c_begin; c < c_end; c++) {
+        const int buf = (int)((c - c_begin) & 1);
+        __syncthreads();  // X planes of chunk c are in buffer buf
+        const bool more = c + 1 < c_end;
+        if (more) {
+            x_fetch(c + 1);
+            if (live) {
+                raw16_load(nxt, W0, r, c + 1, j, K);
+                if constexpr (SW) raw16_load(nxtu, W1, r, c + 1, j, K);
+            }
+        }
+        if (live) {
+            if constexpr (WT == LK_Q8_0) {  // the chunk's block scales: row lane & 15, block j
+                sd[wave][0][j * 16 + (lane & 15)] = lk_h2f((uint16_t)cur.d);
+                if constexpr (SW) sd[wave][NW - 1][j * 16 + (lane & 15)] = lk_h2f((uint16_t)curu.d);
+            }
+            f4 yc[MB], ycu[SW ? MB : 1];
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                yc[m] = f4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (SW) ycu[m] = f4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int blk = 0; blk < 4; blk++) {
+                const h8 wa = raw16_w<WT>(cur, blk);
+                h8 wu;
+                if constexpr (SW) wu = raw16_w<WT>(curu, blk);
+                float4 dv, du;
+                if constexpr (WT == LK_Q8_0) {
+                    dv = *(const float4*)&sd[wave][0][blk * 16 + 4 * j];  // rows 4j..4j+3 of the D layout
+                    if constexpr (SW) du = *(const float4*)&sd[wave][NW - 1][blk * 16 + 4 * j];
+                }
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    const uint32_t xo = (16u * m + ((uint32_t)lane & 15)) * HS + 32 * blk + 8 * j;
+                    const h8 bh = *(const h8*)&xh[buf][xo];
+                    const h8 bl = *(const h8*)&xl[buf][xo];
+                    if constexpr (WT == LK_Q8_0) {
+                        f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bl, D, 0, 0, 0);
+                        yc[m][0] = fmaf(dv.x, D[0], yc[m][0]);
+                        yc[m][1] = fmaf(dv.y, D[1], yc[m][1]);
+                        yc[m][2] = fmaf(dv.z, D[2], yc[m][2]);
+                        yc[m][3] = fmaf(dv.w, D[3], yc[m][3]);
+                        if constexpr (SW) {
+                            f4 E = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            E = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bl, E, 0, 0, 0);
+                            ycu[m][0] = fmaf(du.x, E[0], ycu[m][0]);
+                            ycu[m][1] = fmaf(du.y, E[1], ycu[m][1]);
+                            ycu[m][2] = fmaf(du.z, E[2], ycu[m][2]);
+                            ycu[m][3] = fmaf(du.w, E[3], ycu[m][3]);
+                        }
+                    } else {
+                        yc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, yc[m], 0, 0, 0);
+                        yc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bl, yc[m], 0, 0, 0);
+                        if constexpr (SW) {
+                            ycu[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bh, ycu[m], 0, 0, 0);
+                            ycu[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bl, ycu[m], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            // the chunk's row scales: column b = 16m + (lane & 15)
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const float s = xsc[buf][16 * m + (lane & 15)];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    y[m][i] = fmaf(s, yc[m][i], y[m][i]);
+                    if constexpr (SW) yu[m][i] = fmaf(s, ycu[m][i], yu[m][i]);
+                }
+            }
+        }
+        if (more) {
+            x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
+            cur = nxt;
+            if constexpr (SW) curu = nxtu;
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        const uint32_t b = b0 + 16u * m + ((uint32_t)lane & 15);
+        if (b >= B) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t n = n0 + 4 * j + i;
+            if (n >= a.N) continue;
+            const float v = y[m][i];
+            const float u = SW ? yu[m][i] : 0.f;
+            if (a.ks == 1) {
+                emit(a, MODE, b, n, v, u);
+            } else {
+                const size_t np = SW ? 2 * (size_t)a.N : a.N;
+                float* p = a.part + ((size_t)blockIdx.z * B + b) * np;
+                p[n] = v;
+                if constexpr (SW) p[a.N + n] = u;
+            }
+        }
+    }
+}
+
 // Sums the K-split partials of element (b, n) in split order, then the epilogue.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, int mode) {
     const uint32_t n = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
@@ -211,8 +462,34 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, in
     emit(a, mode, b, n, v, u);
 }
 
+// The f16-rate kernel for Q8_0 and F16 (LKHIP_GEMM=f32 keeps the f32 one).
+static bool gemm16_on(uint32_t type) {
+    if (type != LK_Q8_0 && type != LK_F16) return false;
+    static int on = -1;
+    if (on < 0) {
+        const char* g = getenv("LKHIP_GEMM");
+        on = !(g && strcmp(g, "f32") == 0);
+    }
+    return on == 1;
+}
+
+template <int WT, int MB>
+hipError_t launch_mb16(const LkGemmArgs& a, int mode, dim3 grid, hipStream_t st) {
+    if constexpr (WT == LK_Q8_0 || WT == LK_F16) {
+        switch (mode) {
+        case LK_MV_STORE: hipLaunchKernelGGL((gemm16_kernel<WT, MB, LK_MV_STORE>), grid, dim3(256), 0, st, a); break;
+        case LK_MV_ACC: hipLaunchKernelGGL((gemm16_kernel<WT, MB, LK_MV_ACC>), grid, dim3(256), 0, st, a); break;
+        case LK_MV_SWIGLU: hipLaunchKernelGGL((gemm16_kernel<WT, MB, LK_MV_SWIGLU>), grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
 template <int WT, int MB>
 hipError_t launch_mb(const LkGemmArgs& a, int mode, dim3 grid, hipStream_t st) {
+    if (gemm16_on(WT)) return launch_mb16<WT, MB>(a, mode, grid, st);
     switch (mode) {
     case LK_MV_STORE: hipLaunchKernelGGL((gemm_kernel<WT, MB, LK_MV_STORE>), grid, dim3(256), 0, st, a); break;
     case LK_MV_ACC: hipLaunchKernelGGL((gemm_kernel<WT, MB, LK_MV_ACC>), grid, dim3(256), 0, st, a); break;
