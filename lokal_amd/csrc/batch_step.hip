@@ -41,10 +41,6 @@
 // host reports the failure and falls back to the per-layer launches.
 #include "batch_step.h"
 
-#ifndef LK_BS_FOLD_ORDER
-#define LK_BS_FOLD_ORDER __ATOMIC_ACQ_REL
-#endif
-#define LK_ATTN_FOLD_ORDER LK_BS_FOLD_ORDER
 #include "attention_impl.h"
 #include "gemm_impl.h"
 
