@@ -18,7 +18,8 @@ HBM bytes per launch that rocprofv3 FETCH_SIZE + WRITE_SIZE counted for the
 same command (scaled by the counters' reading for a plain copy of known size;
 see --copy-calibration-mb), read from the committed summary under profiles/.
 `cpu_baseline` is lokal's CPU path (the C oracle: f32 weights expanded at load,
-row-parallel matvec) timed on this host on a bounded sample of the same decode.
+row-parallel matvec) timed on this host over the same positions the GPU line
+times (the window repeated until a bounded budget is spent).
 """
 from __future__ import annotations
 
@@ -90,7 +91,12 @@ def host_cpus() -> dict:
     return info
 
 
-def cpu_baseline(cfg, tensors, prompt_len: int, budget_s: float) -> dict:
+def cpu_baseline(cfg, tensors, prompt, p0: int, n_steps: int, budget_s: float) -> dict:
+    """lokal's CPU path (the C oracle) over the same positions the GPU line
+    times: the same prompt prefilled, greedy decode up to position p0
+    untimed, then the window of positions p0 .. p0 + n_steps - 1 timed, and
+    repeated from p0 (the same tokens rewrite the same cache rows: identical
+    work) until the budget is spent."""
     import oracle
     # the -O3 -mavx2 build of the oracle (bit-identical to the parity build)
     # on every CPU this process may use; a cgroup quota below that caps the
@@ -102,32 +108,35 @@ def cpu_baseline(cfg, tensors, prompt_len: int, budget_s: float) -> dict:
         threads = max(1, min(threads, int(hc["cgroup_quota"])))
     oracle.set_threads(threads)
     om = oracle.Model(cfg, tensors)
-    rng = np.random.default_rng(11)
-    prompt = rng.integers(0, cfg.vocab_size, prompt_len).astype(np.uint32)
-    n_max = 4096
-    s = om.session(prompt_len + n_max + 2)
+    s = om.session(p0 + n_steps + 2)
     lo = s.prefill(prompt)  # untimed, as generate.rs times decode only
     cur = oracle.argmax(lo)
-    # one untimed warm-up token, then time tokens until the budget is spent
-    lo = s.forward(cur, prompt_len)
-    cur = oracle.argmax(lo)
+    for p in range(len(prompt), p0):  # the GPU line's warm-up positions, untimed
+        cur = oracle.argmax(s.forward(cur, p))
+    tok0 = cur
     t0 = time.perf_counter()
-    n = 0
-    while n < n_max:
-        lo = s.forward(cur, prompt_len + 1 + n)
-        cur = oracle.argmax(lo)
-        n += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
+    n, reps = 0, 0
+    while True:
+        cur = tok0
+        for i in range(n_steps):
+            cur = oracle.argmax(s.forward(cur, p0 + i))
+            n += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        else:
+            reps += 1
+            continue
+        break
     dt = time.perf_counter() - t0
     s.close()
     om.close()
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "nproc": hc["nproc"], "affinity_cpus": hc["affinity"], "cgroup_cpu_quota": hc["cgroup_quota"],
             "cpu_model": hc["model"], "build": "gcc -O3 -mavx2 -fopenmp -ffp-contract=off (bit-identical to -O2)",
-            "sample": f"{n} greedy decode tokens after a {prompt_len}-token prefill and 1 warm-up token, "
-                      f"same synthetic Q8_0 weights expanded to f32 (lokal's load_f32 path), "
-                      f"{threads} OpenMP threads, {dt:.1f} s"}
+            "sample": f"{n} greedy decode tokens at positions {p0}..{p0 + n_steps - 1} (the GPU line's timed "
+                      f"positions; {reps} full passes over the window, then part of one), after a "
+                      f"{len(prompt)}-token prefill of the same prompt; same synthetic Q8_0 weights expanded to f32 "
+                      f"(lokal's load_f32 path), {threads} OpenMP threads, {dt:.1f} s"}
 
 
 def main() -> int:
@@ -138,7 +147,6 @@ def main() -> int:
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--cpu-prompt", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -177,6 +185,7 @@ def main() -> int:
     if args.warmup:
         ids = sess.decode_greedy(tok, pos, args.warmup)
         tok, pos = int(ids[-1]), pos + args.warmup
+    timed_p0 = pos
 
     t0 = time.perf_counter()
     ids = sess.decode_greedy(tok, pos, args.steps)  # syncs the stream before returning
@@ -232,6 +241,13 @@ def main() -> int:
             "kernels": [kern("fused_step_kernel", fused_bytes, fused_us, fused_gbs),
                         kern("lm_head_kernel", lm_bytes, lm_us, lm_gbs)],
             "matvec_frac": round(all_gbs / HBM_PEAK_GBS, 4),
+            # each kernel's time is a pair of hipEvents around its launch on
+            # the session's stream, so it also spans the launch gap before the
+            # kernel; their sum against the timed step shows the gaps'
+            # share (rocprofv3's kernel times, under profiles/, exclude them)
+            "timing": "hipEvent pairs around each launch (each spans its launch gap)",
+            "events_sum_us": round(fused_us + lm_us, 2),
+            "step_us": round(dt / args.steps * 1e6, 2),
             "algorithmic_bytes_per_token": mv_bytes,
             "profiled_tokens": int(prof["tokens"]),
         },
@@ -244,7 +260,7 @@ def main() -> int:
     sess.close()
     eng.close()
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, tensors, args.cpu_prompt, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(cfg, tensors, prompt, timed_p0, args.steps, args.cpu_budget)
     del tensors
     print(json.dumps(result), flush=True)
     if args.copy_calibration_mb:

@@ -493,3 +493,57 @@ def test_long_prefill_on_one_thread_while_another_session_decodes():
     a.close()
     b.close()
     eng.close()
+
+
+def test_deferred_argmax_fold_across_calls_and_forward(monkeypatch):
+    """On the one-kernel step the lm_head's per-block argmax keys are folded
+    by the next step's start (or by the finishing launch after a device
+    loop's last step). Greedy ids must not depend on where the calls break:
+    one 24-step call, calls of 1, 2 and 5 steps with a `forward` step and a
+    `decode_greedy` of 0 steps between them, and the collecting-block form
+    (LKHIP_HEAD_DEFER=0) all equal the oracle's ids (f32 caches)."""
+    cfg, tensors, eng, om = build("q8_0", "fused", seed=61)
+    prompt = np.random.default_rng(61).integers(0, cfg.vocab_size, 16).astype(np.uint32)
+    steps = 24
+    o = om.session(16 + steps + 1)
+    lo = o.prefill(prompt)
+    first = int(oracle.argmax(lo))
+    want, cur = [], first
+    for i in range(steps):
+        cur = int(oracle.argmax(o.forward(cur, 16 + i)))
+        want.append(cur)
+
+    def fresh():
+        s = eng.session(16 + steps + 1, kv_dtype="f32")
+        s.prefill(prompt)
+        return s
+
+    s = fresh()
+    assert [int(t) for t in s.decode_greedy(first, 16, steps)] == want
+    s.close()
+
+    s = fresh()
+    got, tok, pos = [], first, 16
+    for n in (1, 2, 0, 5, -1, 1, 3, 0, 2, -1, 1, 7):
+        if n < 0:
+            lg = s.forward(tok, pos)
+            tok, pos = int(np.argmax(lg)), pos + 1
+            got.append(tok)
+        elif n > 0:
+            ids = [int(t) for t in s.decode_greedy(tok, pos, n)]
+            got += ids
+            tok, pos = ids[-1], pos + n
+        else:
+            assert s.decode_greedy(tok, pos, 0).size == 0
+    assert len(got) == steps
+    assert got == want
+    s.close()
+
+    monkeypatch.setenv("LKHIP_HEAD_DEFER", "0")
+    s = fresh()
+    assert [int(t) for t in s.decode_greedy(first, 16, 10)] + \
+        [int(t) for t in s.decode_greedy(want[9], 26, steps - 10)] == want
+    s.close()
+    o.close()
+    eng.close()
+    om.close()
