@@ -479,6 +479,7 @@ def test_batcher_persistent_step_every_row_band(kind, n_rows, monkeypatch):
     sequence over three steps (crossing a 64-position tile for some rows),
     then 8 greedy steps on the device against a per-step host loop."""
     set_batch_path(monkeypatch, "bstep")
+    monkeypatch.setenv("LKHIP_BSTEP_TRACE", "1")  # its barrier times show the step ran
     cfg, eng, om = build(kind, seed=60 + n_rows)
     rng = np.random.default_rng(60 + n_rows)
     lens = [int(rng.integers(1, 140)) for _ in range(n_rows)]
@@ -504,6 +505,8 @@ def test_batcher_persistent_step_every_row_band(kind, n_rows, monkeypatch):
     first = [int(rng.integers(0, cfg.vocab_size)) for _ in lens]
     ids = bat.decode_greedy([BatchRow(first[i], pos[i], int(slots[i])) for i in range(n_rows)], 8)
     assert ids.shape == (8, n_rows)
+    ticks = bat.trace_ticks().astype(np.int64)
+    assert ticks.size == 2 + 5 * cfg.num_hidden_layers and ticks[0] > 0 and np.all(np.diff(ticks) >= 0), ticks
     short = 0
     for i in range(n_rows):
         t, agree = first[i], 8
