@@ -40,23 +40,28 @@ SHAPES = [  # (type, rows, cols)
 
 
 @pytest.mark.parametrize("t,rows,cols", SHAPES)
-def test_matmul_one_hot_is_bit_exact(t, rows, cols):
+@pytest.mark.parametrize("n", [8, 150])
+def test_matmul_one_hot_is_bit_exact(t, rows, cols, n):
+    """One-hot activation rows return weight columns bit for bit (this pins
+    the tile and lane maps); 150 rows take the prefill-sized tiles, with the
+    one-hot rows spread over its column blocks and zero rows between."""
     data = synth.gen_weight(t, 7, f"w{rows}x{cols}", rows, cols).data
     w = K.Weight(t, rows, cols, data)
     ref = dequant(t, data, rows, cols)
     cols_hit = np.array([0, 1, 31, 32, 127, 128, cols // 2 + 3, cols - 1])
-    n = len(cols_hit)
+    at = np.arange(len(cols_hit)) if n == len(cols_hit) else np.array([0, 17, 40, 63, 64, 100, 128, 149])
     x = np.zeros((n, cols), np.float32)
-    x[np.arange(n), cols_hit] = 1.0
+    x[at, cols_hit] = 1.0
     xd, y = K.DeviceArray.from_numpy(x), K.DeviceArray((n, rows))
     K.matmul(w, xd, n, y)
     got = y.numpy()
-    for i, c in enumerate(cols_hit):
+    for i, c in zip(at, cols_hit):
         assert np.array_equal(got[i], ref[:, c]), (i, c)
+    assert not np.delete(got, at, axis=0).any()
 
 
 @pytest.mark.parametrize("t,rows,cols", SHAPES)
-@pytest.mark.parametrize("n_rows", [1, 5, 16, 17, 40])
+@pytest.mark.parametrize("n_rows", [1, 5, 16, 17, 40, 130, 256])
 def test_matmul_matches_float64(t, rows, cols, n_rows):
     data = synth.gen_weight(t, 3, f"w{rows}x{cols}", rows, cols).data
     w = K.Weight(t, rows, cols, data)
@@ -107,6 +112,14 @@ def test_matmul_ragged_rows_and_refusals():
     got = y.numpy()
     assert rel_err(got[:, :rows], x.astype(np.float64) @ dequant(t, data, rows, cols).T) < 1e-5
     assert np.all(got[:, rows:] == 7.0)
+    n2 = 131  # the prefill-sized tiles, ragged in both directions
+    x2 = np.random.default_rng(3).standard_normal((n2, cols)).astype(np.float32)
+    y2 = K.DeviceArray((n2, rows + 8))
+    y2.upload(np.full((n2, rows + 8), 7.0, np.float32))
+    K.matmul(w, K.DeviceArray.from_numpy(x2), n2, y2, ldy=rows + 8)
+    got2 = y2.numpy()
+    assert rel_err(got2[:, :rows], x2.astype(np.float64) @ dequant(t, data, rows, cols).T) < 1e-5
+    assert np.all(got2[:, rows:] == 7.0)
     with pytest.raises(LokalHipError, match="multiple of 4"):
         K.matmul(w, K.DeviceArray((n, 70)), n, y, ldx=66)
 
