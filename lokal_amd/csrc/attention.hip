@@ -267,29 +267,37 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 //            disjoint LDS banks.
 // At GQA 7 this is ~1/5 of the vector-ALU work of the scalar kernel, whose
 // FMA rate per HBM byte is close to the ALU's.
-template <int G>
+template <int G, int PR>
 __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs a) {
-    attn_mfma_item<G>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+    attn_mfma_item<G, PR>(a, blockIdx.x, blockIdx.y, blockIdx.z * PR);
 }
+// Rows per item of a grouped (prefill) launch: as many as fill the 16 MFMA columns.
+static constexpr uint32_t attn_rows_per_item(uint32_t G) { return 16 / G; }
 
 hipError_t lk_attn_launch(const LkAttnArgs& args, hipStream_t st) {
     if (args.n_kv == 0 || args.n_heads % args.n_kv || !args.cnt || !args.max_seq) return hipErrorInvalidValue;
     LkAttnArgs a = args;
-    const AttnPlan p = attn_plan(a.n_seq, a.n_kv, a.max_seq);
-    a.waves = p.waves;
-    a.tiles = p.tiles;
-    a.cstride = attn_chunk_cap(a.max_seq);
     const uint32_t G = a.n_heads / a.n_kv;
-    dim3 grid(p.chunks, a.n_kv, a.n_seq);
     // The matrix-core kernel is the faster one at every context measured (4
     // sequences x 24 layers: 268 vs 327 us per step at ctx 4096, 562 vs 690
     // at 32768); LKHIP_ATTN=valu selects the vector-ALU kernel.
     const char* fe = getenv("LKHIP_ATTN");
     const bool mfma = !(fe && strcmp(fe, "valu") == 0);
+    // a prefill chunk on the matrix-core kernel: several rows per item, so a
+    // K/V tile is read once for all of them
+    const bool group = a.grouped && !a.kv_f32 && mfma && G <= 8;
+    const uint32_t pr = group ? attn_rows_per_item(G) : 1;
+    const uint32_t items = (a.n_seq + pr - 1) / pr;
+    const AttnPlan p = attn_plan(items, a.n_kv, a.max_seq);
+    a.waves = p.waves;
+    a.tiles = p.tiles;
+    a.cstride = attn_chunk_cap(a.max_seq);
+    dim3 grid(p.chunks, a.n_kv, items);
 #define LK_ATTN_CASE(g)                                                                         \
     case g:                                                                                     \
         if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(LK_AW * 64), 0, st, a); \
-        else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g>), grid, dim3(LK_AW * 64), 0, st, a);     \
+        else if (group) hipLaunchKernelGGL((attn_mfma_kernel<g, attn_rows_per_item(g)>), grid, dim3(LK_AW * 64), 0, st, a); \
+        else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g, 1>), grid, dim3(LK_AW * 64), 0, st, a);     \
         else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(LK_AW * 64), 0, st, a);  \
         break;
     switch (G) {

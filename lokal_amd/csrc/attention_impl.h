@@ -71,7 +71,10 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
 #define LK_ATTN_FOLD_ORDER __ATOMIC_RELAXED
 #endif
 
-template <int G>
+// PR > 1: the item covers rows seq .. seq + PR - 1 (consecutive positions of
+// one sequence, a prefill chunk), column c = (row c / G, head c % G); the
+// count is the first row's.
+template <int G, int PR = 1>
 __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t nch) {
     __shared__ uint32_t last;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -85,11 +88,13 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
     __syncthreads();
     if (!last) return;
 #pragma unroll
-    for (int r = 0; r < (8 + LK_AW - 1) / LK_AW; r++) {
-        const uint32_t g = (uint32_t)w + LK_AW * r;
-        if (g >= (uint32_t)G) break;
+    for (int r = 0; r < (G * PR + LK_AW - 1) / LK_AW; r++) {
+        const uint32_t cg = (uint32_t)w + LK_AW * r;
+        if (cg >= (uint32_t)(G * PR)) break;
+        const uint32_t rs = seq + cg / G, g = cg % G;
+        if (rs >= a.n_seq) break;  // a ragged last group
         const uint32_t h = kvh * G + g;
-        const float* ph = a.part + ((size_t)seq * a.n_heads + h) * a.cstride * (2 + LK_HD);
+        const float* ph = a.part + ((size_t)rs * a.n_heads + h) * a.cstride * (2 + LK_HD);
         const bool live = (uint32_t)lane < nch;
         const float* pk = ph + (size_t)(live ? lane : 0) * (2 + LK_HD);
         const float mk = ld_coherent(pk), lk = ld_coherent(pk + 1);
@@ -110,7 +115,7 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
         }
         // write-through: read by another XCD later in the same launch (the
         // persistent Batcher step's o_proj phase)
-        st_coherent(a.out + ((size_t)seq * a.n_heads + h) * LK_HD + lane, A / L);
+        st_coherent(a.out + ((size_t)rs * a.n_heads + h) * LK_HD + lane, A / L);
     }
     if (tid == 0)
         __hip_atomic_store(a.cnt + ((size_t)seq * a.n_kv + kvh) * LK_ATTN_CNT_STRIDE, 0u, __ATOMIC_RELAXED,
@@ -119,12 +124,16 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
 
 // The 4 waves' (m, l, acc) of each head (red_m[w][g] etc.) -> the chunk's
 // partial per head, with coherent stores.
-template <int G, typename RM, typename RA>
+// PR > 1: columns c = (row seq + c / G, head c % G), as in count_in_and_fold.
+template <int G, int PR = 1, typename RM, typename RA>
 __device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t chunk,
                                                     const RM& red_m, const RM& red_l, const RA& red_acc) {
-    float* part = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * a.cstride + chunk) * (2 + LK_HD);
-    for (int t = threadIdx.x; t < G * LK_HD; t += LK_AW * 64) {
-        const int g = t / LK_HD, d = t % LK_HD;
+    for (int t = threadIdx.x; t < G * PR * LK_HD; t += LK_AW * 64) {
+        const int g = t / LK_HD, d = t % LK_HD;  // g: the column
+        const uint32_t rs = seq + (uint32_t)g / G;
+        if (rs >= a.n_seq) break;  // a ragged last group (t only grows)
+        float* part = a.part + (((size_t)rs * a.n_heads + (size_t)kvh * G + (uint32_t)g % G) * a.cstride + chunk) *
+                                   (2 + LK_HD);
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
@@ -137,7 +146,7 @@ __device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_
                 A = fmaf(sc, red_acc[ww][g][d], A);
             }
         }
-        float* ph = part + (size_t)g * a.cstride * (2 + LK_HD);
+        float* ph = part;
         if (d == 0) {
             st_coherent(ph, M);
             st_coherent(ph + 1, L);
@@ -160,10 +169,17 @@ __device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
 // One (chunk, kv head, sequence) item of the f16-cache partial on the matrix
 // cores, by a block of LK_AW waves: attn_mfma_kernel runs one item per block;
 // the Batcher's persistent step (batch_step.hip) runs them in its attention
-// phase.
-template <int G>
+// phase.  PR > 1 (a prefill chunk: rows seq .. seq + PR - 1 are consecutive
+// positions of one sequence, so they share its K/V): the item takes the PR
+// rows' G heads as the MFMA's G * PR <= 16 columns, column c = (row c / G,
+// head c % G), and each K/V tile is read once for all of them; a column's
+// positions past its own row's are masked (causal).
+template <int G, int PR = 1>
 __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chunk, uint32_t kvh, uint32_t seq) {
-    const uint32_t ctx = attn_ctx(a, seq);
+    static_assert(G * PR <= 16, "the item's columns fit one 16-column MFMA tile");
+    // the item's context: its last row's (positions grow along the rows)
+    const uint32_t rlast = seq + PR - 1 < a.n_seq ? seq + PR - 1 : a.n_seq - 1;
+    const uint32_t ctx = attn_ctx(a, rlast);
     const uint32_t A = a.waves, T = a.tiles, CH = 64 * A * T;
     const uint32_t c0 = chunk * CH;
     if (c0 >= ctx) return;  // uniform over the block
@@ -183,11 +199,16 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t j = (uint32_t)lane >> 4, c16 = (uint32_t)lane & 15;
     const uint32_t plast = ctx - 1;
+    // this lane's column: row seq + crow, head cg; live columns c16 < G * PR
+    // of rows inside the call
+    const uint32_t crow = c16 / G < (uint32_t)PR ? c16 / G : 0, cg = c16 % G;
+    const bool clive = c16 < (uint32_t)(G * PR) && seq + crow < a.n_seq;
+    const uint32_t cctx = PR > 1 ? attn_ctx(a, clive ? seq + crow : seq) : ctx;  // the column's causal bound
 
-    // q of head c16 (zero past G), dims 16j + 4s .. +3 for step s, as f16 hi + lo
+    // q of column c16 (zero for a dead column), dims 16j + 4s .. +3 for step s, as f16 hi + lo
     lk_h4 qh[4], ql[4];
     {
-        const float* qrow = a.q + (size_t)seq * a.q_stride + ((size_t)kvh * G + (c16 < (uint32_t)G ? c16 : 0)) * LK_HD;
+        const float* qrow = a.q + (size_t)(seq + (clive ? crow : 0)) * a.q_stride + ((size_t)kvh * G + cg) * LK_HD;
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             // coherent: q may have been written earlier in the same launch
@@ -196,7 +217,7 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
                                 ld_coherent(qrow + 16 * j + 4 * st + 2), ld_coherent(qrow + 16 * j + 4 * st + 3)};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float xv = c16 < (uint32_t)G ? x[e] : 0.f;
+                const float xv = clive ? x[e] : 0.f;
                 const _Float16 hi = (_Float16)xv;
                 qh[st][e] = hi;
                 ql[st][e] = (_Float16)(xv - (float)hi);
@@ -255,13 +276,17 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t p = p0 + 16u * t + 4u * (uint32_t)i + j;  // MFMA row 4j + i
-                const float v = p < ctx ? sc[t][i] * 0.125f : -INFINITY;
+                const float v = p < cctx ? sc[t][i] * 0.125f : -INFINITY;
                 sc[t][i] = v;
                 mx = fmaxf(mx, v);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(mt, mx);    // finite: the tile holds a live position
+        // finite for PR == 1: the tile holds a live position.  PR > 1: a
+        // column may have none yet (its row ends before the tile); it keeps
+        // (-inf, 0, 0) with any finite reference for the exponentials
+        const float mn0 = fmaxf(mt, mx);
+        const float mn = (PR > 1 && mn0 == -INFINITY) ? 0.f : mn0;
         const float fo = expf(mt - mn);    // the running sums' factor (0 on the first tile)
         float sum = 0.f;
         lk_h4 ph[4], pl[4];
@@ -278,7 +303,7 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
         lt = fmaf(lt, fo, sum);
-        mt = mn;
+        mt = mn0;
         // O's heads are 4j + i: their factors live on lanes 4j + i
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -317,6 +342,6 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
 #pragma unroll
         for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][4 * c16 + d] = o[d][i];
     __syncthreads();
-    write_chunk_partial<G>(a, seq, kvh, chunk, red_m, red_l, red_acc);
-    count_in_and_fold<G>(a, seq, kvh, nch);
+    write_chunk_partial<G, PR>(a, seq, kvh, chunk, red_m, red_l, red_acc);
+    count_in_and_fold<G, PR>(a, seq, kvh, nch);
 }

@@ -1252,8 +1252,10 @@ static hipError_t enqueue_rows_head(const lkhip_engine* e, Rows& R, uint32_t n, 
     return rows_gemm(R, a, LK_MV_STORE, st);
 }
 
+// one_seq: the rows are consecutive positions of one sequence (a prefill
+// chunk), which lets the attention read each K/V tile once for several rows.
 static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const KvDesc& kv, int head,
-                               hipStream_t st) {
+                               hipStream_t st, bool one_seq) {
     const lkhip_config& c = e->cfg;
     const uint32_t h = c.hidden_size, I = c.intermediate_size, qd = e->qd, kvd = e->kvd;
     const uint32_t qkvd = qd + 2 * kvd, cap = R.cap;
@@ -1329,6 +1331,7 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             lk_attn_bind_scratch(a, R.apart.as<float>(), (size_t)R.cap * c.num_key_value_heads);
             a.seq_stride = kv.slot_elems;
             a.q_stride = qkvd;
+            a.grouped = one_seq ? 1u : 0u;
             RSTEP(lk_attn_launch(a, st));
         }
         {
@@ -1412,7 +1415,7 @@ static int rows_prefill(const lkhip_engine* e, Rows& R, const KvDesc& kv, uint32
         // Through the gate: a long prefill on this stream must not hold CUs while
         // another stream's one-kernel step needs every workgroup resident.
         rc = gated_launch(e->device, st, [&]() -> int {
-            hipError_t err = enqueue_rows(e, R, m, kv, last && logits_out ? HEAD_LAST : HEAD_NONE, st);
+            hipError_t err = enqueue_rows(e, R, m, kv, last && logits_out ? HEAD_LAST : HEAD_NONE, st, true);
             if (err != hipSuccess)
                 return fail(LKHIP_E_HIP, "batched prefill launch failed: %s", hipGetErrorString(err));
             return LKHIP_OK;
@@ -1506,7 +1509,7 @@ extern "C" int lkhip_session_forward_batch(lkhip_session* s, const uint32_t* ids
         for (uint32_t i = 0; i < m; i++) pos[i] = pos0 + off + i;
         if ((rc = rows_upload(R, ids + off, pos.data(), slots.data(), m, s->stream))) return rc;
         rc = gated_launch(s->e->device, s->stream, [&]() -> int {
-            hipError_t err = enqueue_rows(s->e, R, m, kv, HEAD_ALL, s->stream);
+            hipError_t err = enqueue_rows(s->e, R, m, kv, HEAD_ALL, s->stream, true);
             if (err != hipSuccess) return fail(LKHIP_E_HIP, "forward_batch launch failed: %s", hipGetErrorString(err));
             return LKHIP_OK;
         });
@@ -1819,7 +1822,7 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, int path 
         hipError_t err;
         if (path == PATH_BSTEP) err = batch_enqueue_bstep(b, n, st);
         else if (path == PATH_FUSED) err = n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st);
-        else err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st);
+        else err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st, false);
         if (err == hipSuccess && path != PATH_LAYERS)
             err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;

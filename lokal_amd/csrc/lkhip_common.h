@@ -248,6 +248,10 @@ struct LkAttnArgs {
     uint64_t q_stride;      // floats between two sequences' q rows (out rows are n_heads * 64 apart)
     uint32_t kv_f32;        // 1: the cache holds f32, 0: f16
     uint32_t waves, tiles, cstride;  // set by lk_attn_launch: its chunk plan and partial slots per head
+    // 1: rows i, i+1, ... are consecutive positions of one sequence (a
+    // prefill chunk: one slot, ctx_len[i] + 1 == ctx_len[i + 1]), so an item
+    // may take several rows at once (f16 cache, matrix-core kernel)
+    uint32_t grouped;
 };
 uint32_t lk_attn_chunk(uint32_t max_seq);
 // Sets a's chunk plan (waves, tiles, cstride) for its n_seq, n_kv and
