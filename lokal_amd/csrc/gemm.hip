@@ -97,7 +97,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
             uint32_t bb = b0 + row;
             bb = bb < B ? bb : B - 1;
             const uint32_t k = c * KC + col;
-            xv[i] = k < K ? *(const float4*)(a.x + (size_t)bb * a.ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            // the load is unconditional (an in-range address), its value
+            // dropped past K: a load under a branch makes the compiler wait
+            // for every load in flight where the paths meet
+            const float4 v = *(const float4*)(a.x + (size_t)bb * a.ldx + (k < K ? k : 0));
+            xv[i] = k < K ? v : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto x_store = [&](int buf) {
@@ -119,26 +123,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
         acc[m] = f4{0.f, 0.f, 0.f, 0.f};
         if constexpr (SW) accu[m] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    // Loads are issued unconditionally (dead waves read in-range addresses
+    // whose values go unused), so the wait before a chunk's MFMAs counts only
+    // the loads issued before the next chunk's; a load under a branch would
+    // make the compiler wait for every load in flight where the paths meet.
     Raw<WT> cur, nxt, curu, nxtu;
     if (c_begin < c_end) {
         x_fetch(c_begin);
         x_store(0);
-        if (live) {
-            raw_load(cur, W0, r, kb_of(c_begin));
-            if constexpr (SW) raw_load(curu, W1, r, kb_of(c_begin));
-        }
+        raw_load(cur, W0, r, kb_of(c_begin));
+        if constexpr (SW) raw_load(curu, W1, r, kb_of(c_begin));
     }
-    for (uint32_t c = c_begin; c < c_end; c++) {
-        const int buf = (int)((c - c_begin) & 1);
-        __syncthreads();  // X tile of chunk c is in xs[buf]
-        const bool more = c + 1 < c_end;
-        if (more) {
-            x_fetch(c + 1);
-            if (live) {
-                raw_load(nxt, W0, r, kb_of(c + 1));
-                if constexpr (SW) raw_load(nxtu, W1, r, kb_of(c + 1));
-            }
-        }
+    // one chunk's MFMAs on cur and X buffer buf
+    auto chunk = [&](uint32_t c, int buf) {
         if (live) {
             const uint32_t kb = kb_of(c);
             const bool ok = c * KC + 32 * j < K;
@@ -167,11 +164,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
                 }
             }
         }
-        if (more) {
-            x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
-            cur = nxt;
-            if constexpr (SW) curu = nxtu;
-        }
+    };
+    // every chunk but the last prefetches the next one's X and weights
+    uint32_t c = c_begin;
+    for (; c + 1 < c_end; c++) {
+        const int buf = (int)((c - c_begin) & 1);
+        __syncthreads();  // X tile of chunk c is in xs[buf]
+        x_fetch(c + 1);
+        raw_load(nxt, W0, r, kb_of(c + 1));
+        if constexpr (SW) raw_load(nxtu, W1, r, kb_of(c + 1));
+        chunk(c, buf);
+        x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
+        cur = nxt;
+        if constexpr (SW) curu = nxtu;
+    }
+    if (c < c_end) {
+        __syncthreads();  // X tile of chunk c is in xs[buf]
+        chunk(c, (int)((c - c_begin) & 1));
     }
     if (!live) return;
 
@@ -303,7 +312,8 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
             uint32_t bb = b0 + row;
             bb = bb < B ? bb : B - 1;
             const uint32_t k = c * KC + col;
-            xv[i] = k < K ? *(const float4*)(a.x + (size_t)bb * a.ldx + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 v = *(const float4*)(a.x + (size_t)bb * a.ldx + (k < K ? k : 0));  // unconditional
+            xv[i] = k < K ? v : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto x_store = [&](int buf) {
@@ -336,26 +346,16 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
         y[m] = f4{0.f, 0.f, 0.f, 0.f};
         if constexpr (SW) yu[m] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    // unconditional loads, as in gemm_kernel
     Raw16<WT> cur, nxt, curu, nxtu;
     if (c_begin < c_end) {
         x_fetch(c_begin);
         x_store(0);
-        if (live) {
-            raw16_load(cur, W0, r, c_begin, j, K);
-            if constexpr (SW) raw16_load(curu, W1, r, c_begin, j, K);
-        }
+        raw16_load(cur, W0, r, c_begin, j, K);
+        if constexpr (SW) raw16_load(curu, W1, r, c_begin, j, K);
     }
-    for (uint32_t c = c_begin; c < c_end; c++) {
-        const int buf = (int)((c - c_begin) & 1);
-        __syncthreads();  // X planes of chunk c are in buffer buf
-        const bool more = c + 1 < c_end;
-        if (more) {
-            x_fetch(c + 1);
-            if (live) {
-                raw16_load(nxt, W0, r, c + 1, j, K);
-                if constexpr (SW) raw16_load(nxtu, W1, r, c + 1, j, K);
-            }
-        }
+    // one chunk's MFMAs on cur and X buffer buf
+    auto chunk = [&](uint32_t c, int buf) {
         if (live) {
             if constexpr (WT == LK_Q8_0) {  // the chunk's block scales: row lane & 15, block j
                 sd[wave][0][j * 16 + (lane & 15)] = lk_h2f((uint16_t)cur.d);
@@ -418,11 +418,23 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
                 }
             }
         }
-        if (more) {
-            x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
-            cur = nxt;
-            if constexpr (SW) curu = nxtu;
-        }
+    };
+    // every chunk but the last prefetches the next one's X and weights
+    uint32_t c = c_begin;
+    for (; c + 1 < c_end; c++) {
+        const int buf = (int)((c - c_begin) & 1);
+        __syncthreads();  // X planes of chunk c are in buffer buf
+        x_fetch(c + 1);
+        raw16_load(nxt, W0, r, c + 1, j, K);
+        if constexpr (SW) raw16_load(nxtu, W1, r, c + 1, j, K);
+        chunk(c, buf);
+        x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
+        cur = nxt;
+        if constexpr (SW) curu = nxtu;
+    }
+    if (c < c_end) {
+        __syncthreads();  // X planes of chunk c are in buffer buf
+        chunk(c, (int)((c - c_begin) & 1));
     }
     if (!live) return;
 #pragma unroll
