@@ -488,7 +488,7 @@ __device__ __forceinline__ void lin_phase(const LkBatchStepArgs& a, const Lin& g
 
 template <int WT, int G, int MB>
 __global__ __launch_bounds__(BTH, 1) void batch_step_kernel(const LkBatchStepArgs a) {
-    extern __shared__ float dyn[];
+    extern __shared__ __align__(16) float dyn[];  // 16-byte aligned after the static LDS
     LinLds& S = *(LinLds*)dyn;
     const uint32_t B = a.nrows, h = a.h, I = a.I;
     const uint32_t qd = a.nh * 64, kvd = a.nkv * 64, qkvd = qd + 2 * kvd;

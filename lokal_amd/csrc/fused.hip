@@ -96,7 +96,7 @@ __device__ __forceinline__ float await_x(const Ctx& c, const uint64_t* p, uint32
 
 template <int WT, int NCHH, int NCHI, typename KV, int G>
 __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];  // 16-byte aligned after the static LDS (16-byte LDS accesses)
     const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
     const uint32_t vmax = (I > h ? I : h) > qd ? (I > h ? I : h) : qd;

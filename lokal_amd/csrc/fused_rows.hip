@@ -40,7 +40,7 @@ using namespace lk;
 
 template <int WT, int NCHH, int NCHI, int G, int NB>
 __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];  // 16-byte aligned after the static LDS (16-byte LDS accesses)
     const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
     // the down stage takes its input S6R rows at a time, so that NB = 8 fits

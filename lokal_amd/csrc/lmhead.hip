@@ -47,7 +47,7 @@ __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a >
 
 template <int WT, int NCH, int R>
 __global__ __launch_bounds__(HT) void lm_head_kernel(const LkHeadArgs a) {
-    extern __shared__ float xn[];  // h floats
+    extern __shared__ __align__(16) float xn[];  // h floats; 16-byte aligned after the static LDS
     __shared__ float red[HW];
     __shared__ uint64_t bk[HW];
     __shared__ int to_any;
