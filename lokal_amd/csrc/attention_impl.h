@@ -91,8 +91,8 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
     for (int r = 0; r < (G * PR + LK_AW - 1) / LK_AW; r++) {
         const uint32_t cg = (uint32_t)w + LK_AW * r;
         if (cg >= (uint32_t)(G * PR)) break;
-        const uint32_t rs = seq + cg / G, g = cg % G;
-        if (rs >= a.n_seq) break;  // a ragged last group
+        const uint32_t rs = PR == 1 ? seq : seq + cg / G, g = PR == 1 ? cg : cg % G;
+        if (PR > 1 && rs >= a.n_seq) break;  // a ragged last group
         const uint32_t h = kvh * G + g;
         const float* ph = a.part + ((size_t)rs * a.n_heads + h) * a.cstride * (2 + LK_HD);
         const bool live = (uint32_t)lane < nch;
@@ -128,12 +128,18 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
 template <int G, int PR = 1, typename RM, typename RA>
 __device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t chunk,
                                                     const RM& red_m, const RM& red_l, const RA& red_acc) {
+    float* const part1 = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * a.cstride + chunk) * (2 + LK_HD);
     for (int t = threadIdx.x; t < G * PR * LK_HD; t += LK_AW * 64) {
         const int g = t / LK_HD, d = t % LK_HD;  // g: the column
-        const uint32_t rs = seq + (uint32_t)g / G;
-        if (rs >= a.n_seq) break;  // a ragged last group (t only grows)
-        float* part = a.part + (((size_t)rs * a.n_heads + (size_t)kvh * G + (uint32_t)g % G) * a.cstride + chunk) *
-                                   (2 + LK_HD);
+        float* part;
+        if constexpr (PR == 1) {
+            part = part1 + (size_t)g * a.cstride * (2 + LK_HD);
+        } else {
+            const uint32_t rs = seq + (uint32_t)g / G;
+            if (rs >= a.n_seq) break;  // a ragged last group (t only grows)
+            part = a.part + (((size_t)rs * a.n_heads + (size_t)kvh * G + (uint32_t)g % G) * a.cstride + chunk) *
+                                (2 + LK_HD);
+        }
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < LK_AW; ww++) M = fmaxf(M, red_m[ww][g]);
@@ -178,7 +184,7 @@ template <int G, int PR = 1>
 __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chunk, uint32_t kvh, uint32_t seq) {
     static_assert(G * PR <= 16, "the item's columns fit one 16-column MFMA tile");
     // the item's context: its last row's (positions grow along the rows)
-    const uint32_t rlast = seq + PR - 1 < a.n_seq ? seq + PR - 1 : a.n_seq - 1;
+    const uint32_t rlast = PR == 1 ? seq : (seq + PR - 1 < a.n_seq ? seq + PR - 1 : a.n_seq - 1);
     const uint32_t ctx = attn_ctx(a, rlast);
     const uint32_t A = a.waves, T = a.tiles, CH = 64 * A * T;
     const uint32_t c0 = chunk * CH;
@@ -201,14 +207,15 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
     const uint32_t plast = ctx - 1;
     // this lane's column: row seq + crow, head cg; live columns c16 < G * PR
     // of rows inside the call
-    const uint32_t crow = c16 / G < (uint32_t)PR ? c16 / G : 0, cg = c16 % G;
-    const bool clive = c16 < (uint32_t)(G * PR) && seq + crow < a.n_seq;
+    const uint32_t crow = PR == 1 ? 0 : (c16 / G < (uint32_t)PR ? c16 / G : 0);
+    const uint32_t cg = PR == 1 ? (c16 < (uint32_t)G ? c16 : 0) : c16 % G;
+    const bool clive = PR == 1 ? c16 < (uint32_t)G : (c16 < (uint32_t)(G * PR) && seq + crow < a.n_seq);
     const uint32_t cctx = PR > 1 ? attn_ctx(a, clive ? seq + crow : seq) : ctx;  // the column's causal bound
 
     // q of column c16 (zero for a dead column), dims 16j + 4s .. +3 for step s, as f16 hi + lo
     lk_h4 qh[4], ql[4];
     {
-        const float* qrow = a.q + (size_t)(seq + (clive ? crow : 0)) * a.q_stride + ((size_t)kvh * G + cg) * LK_HD;
+        const float* qrow = a.q + (size_t)(seq + (clive ? crow : 0u)) * a.q_stride + ((size_t)kvh * G + cg) * LK_HD;
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             // coherent: q may have been written earlier in the same launch
