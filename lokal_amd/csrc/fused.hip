@@ -129,14 +129,37 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
     // is not a power of two.
     const uint32_t xcd = __builtin_amdgcn_s_getreg(LK_HWREG_XCC_ID) & (LK_XCDS - 1);
     const uint32_t nslot = gridDim.x / LK_XCDS;
+    // The slot counter, the session's step state, the lm_head keys to fold
+    // and the layer descriptors are loaded together: one memory round trip
+    // before the fold and the first rows, not one after another.
+    uint32_t slot_raw = 0;
     if (threadIdx.x == 0)
-        *slot_lds = __builtin_amdgcn_atomic_inc32(a.xcd_cnt + xcd * LK_XCD_CNT_STRIDE, nslot - 1,
-                                                  __ATOMIC_RELAXED, "agent") % nslot;
+        slot_raw = __builtin_amdgcn_atomic_inc32(a.xcd_cnt + xcd * LK_XCD_CNT_STRIDE, nslot - 1, __ATOMIC_RELAXED,
+                                                 "agent");
+    static_assert(LK_HEAD_MAX_BLOCKS <= 2 * FT, "two lm_head blocks' keys per thread");
+    uint4 s0 = make_uint4(0, 0, 0, 0);  // token, pos, n_out, n_feed
+    uint2 s1 = make_uint2(0, 0);        // fed, pending
+    uint64_t kw[4] = {0, 0, 0, 0};
+    uint32_t hep = 0;  // the epoch of the keys to fold
+    if (!a.meta) {
+        s0 = *(const uint4*)lk_g((const uint32_t*)a.st);
+        s1 = *(const uint2*)lk_g((const uint32_t*)a.st + 4);
+        if (a.head_keys) {
+            hep = *lk_g(a.head_epoch) + 1;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t i = threadIdx.x + (uint32_t)(k >> 1) * FT;
+                if (i < a.head_blocks)
+                    kw[k] = __hip_atomic_load(a.head_keys + 2 * i + (k & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
     {
         const uint32_t* src = (const uint32_t*)a.layers;
         uint32_t* dst = (uint32_t*)lay;
         const uint32_t n32 = a.n_layers * (uint32_t)(sizeof(LkFusedLayer) / 4);
         for (uint32_t i = threadIdx.x; i < n32; i += FT) dst[i] = src[i];
+        if (threadIdx.x == 0) *slot_lds = slot_raw % nslot;
         lds_barrier();
     }
 
@@ -160,23 +183,8 @@ __global__ __launch_bounds__(FT, 1) void fused_step_kernel(const LkFusedArgs a) 
         pos = __builtin_amdgcn_readfirstlane(a.meta[a.meta_cap]);
         slot = __builtin_amdgcn_readfirstlane(a.meta[2 * a.meta_cap]);
     } else {
-        // the state, the key epoch and this thread's key words are loaded
-        // together (the keys whether or not they turn out to be pending), so
-        // the fold costs one memory round trip before the embedding row
-        const uint4 s0 = *(const uint4*)lk_g((const uint32_t*)a.st);
-        const uint2 s1 = *(const uint2*)lk_g((const uint32_t*)a.st + 4);  // fed, pending
-        static_assert(LK_HEAD_MAX_BLOCKS <= 2 * FT, "two lm_head blocks' keys per thread");
-        uint64_t kw[4] = {0, 0, 0, 0};
-        uint32_t hep = 0;  // the epoch of the keys to fold
-        if (a.head_keys) {
-            hep = *lk_g(a.head_epoch) + 1;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t i = threadIdx.x + (uint32_t)(k >> 1) * FT;
-                if (i < a.head_blocks)
-                    kw[k] = __hip_atomic_load(a.head_keys + 2 * i + (k & 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
+        // the state, the key epoch and this thread's key words were loaded
+        // at the start (the keys whether or not they turn out to be pending)
         token = s0.x;
         pos = s0.y;
         n_out = s0.z;
