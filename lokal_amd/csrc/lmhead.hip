@@ -115,23 +115,8 @@ __global__ __launch_bounds__(HT) void lm_head_kernel(const LkHeadArgs a) {
                 xr[i][16 + e] = ok ? xl[32 + e] : 0.f;
             }
         } else {
-            // CE consecutive floats per lane, 4 at a time, lane l starting at
-            // group l & 3 of its run: lanes 64 B apart would otherwise hit the
-            // same LDS banks in every 16-byte read
-            const float* xl = xn + (ok ? ch * CE : 0);
 #pragma unroll
-            for (int g = 0; g < (int)CE / 4; g++) {
-                const int gg = (g + lane) & ((int)CE / 4 - 1);
-                const float4 v = *(const float4*)(xl + 4 * gg);
-#pragma unroll
-                for (int q = 0; q < (int)CE / 4; q++)
-                    if (q == gg) {
-                        xr[i][4 * q] = ok ? v.x : 0.f;
-                        xr[i][4 * q + 1] = ok ? v.y : 0.f;
-                        xr[i][4 * q + 2] = ok ? v.z : 0.f;
-                        xr[i][4 * q + 3] = ok ? v.w : 0.f;
-                    }
-            }
+            for (int e = 0; e < (int)CE; e++) xr[i][e] = ok ? xn[ch * CE + e] : 0.f;
         }
     }
 
