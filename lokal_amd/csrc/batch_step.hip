@@ -198,7 +198,8 @@ __device__ __forceinline__ void lin_item(const LkBatchStepArgs& a, const Lin& g,
             const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
             const uint32_t bb = b0 + row < B ? b0 + row : B - 1;
             const uint32_t k = c * KC + col;
-            xv[i] = k < K ? ld4(xr, (bb * g.ldx + k) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 v = ld4(xr, (bb * g.ldx + (k < K ? k : 0)) * 4);  // unconditional, dropped past K
+            xv[i] = k < K ? v : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto x_store = [&](int buf) {
@@ -217,14 +218,13 @@ __device__ __forceinline__ void lin_item(const LkBatchStepArgs& a, const Lin& g,
             const uint32_t e = threadIdx.x + BTH * i;
             const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
             const uint32_t k = c * KC + col;
-            if (k < K) {
-                const float4 gv = *(const float4*)(g.gain + k);
-                const float s = S.scale[row];
-                xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, s), gv.x);
-                xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, s), gv.y);
-                xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, s), gv.z);
-                xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, s), gv.w);
-            }
+            // past K x is zero, so any in-range gain leaves it zero
+            const float4 gv = *(const float4*)(g.gain + (k < K ? k : 0));
+            const float s = S.scale[row];
+            xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, s), gv.x);
+            xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, s), gv.y);
+            xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, s), gv.z);
+            xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, s), gv.w);
         }
     };
     auto kb_of = [&](uint32_t c) -> uint32_t {
@@ -238,28 +238,21 @@ __device__ __forceinline__ void lin_item(const LkBatchStepArgs& a, const Lin& g,
         acc[m] = f4{0.f, 0.f, 0.f, 0.f};
         accu[m] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    // Loads are issued unconditionally (dead waves read in-range rows whose
+    // values go unused) and the last chunk is peeled, so the wait before a
+    // chunk's MFMAs leaves the next chunk's loads in flight; a load under a
+    // branch would make the compiler wait for every load where paths meet.
     Raw<WT> cur, nxt, curu, nxtu;
     __syncthreads();  // the scales are in LDS; the previous item is done with xs
     if (c_begin < c_end) {
         x_fetch(c_begin);
         x_norm(c_begin);
         x_store(0);
-        if (live) {
-            lkg::raw_load(cur, W0, r, kb_of(c_begin));
-            if constexpr (SW) lkg::raw_load(curu, W1, r, kb_of(c_begin));
-        }
+        lkg::raw_load(cur, W0, r, kb_of(c_begin));
+        if constexpr (SW) lkg::raw_load(curu, W1, r, kb_of(c_begin));
     }
-    for (uint32_t c = c_begin; c < c_end; c++) {
-        const int buf = (int)((c - c_begin) & 1);
-        __syncthreads();  // X tile of chunk c is in xs[buf]
-        const bool more = c + 1 < c_end;
-        if (more) {
-            x_fetch(c + 1);
-            if (live) {
-                lkg::raw_load(nxt, W0, r, kb_of(c + 1));
-                if constexpr (SW) lkg::raw_load(nxtu, W1, r, kb_of(c + 1));
-            }
-        }
+    // one chunk's MFMAs on cur and X buffer buf
+    auto chunk = [&](uint32_t c, int buf) {
         if (live) {
             const uint32_t kb = kb_of(c);
             const bool ok = c * KC + 32 * j < K;
@@ -288,12 +281,23 @@ __device__ __forceinline__ void lin_item(const LkBatchStepArgs& a, const Lin& g,
                 }
             }
         }
-        if (more) {
-            x_norm(c + 1);
-            x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
-            cur = nxt;
-            if constexpr (SW) curu = nxtu;
-        }
+    };
+    uint32_t c = c_begin;
+    for (; c + 1 < c_end; c++) {
+        const int buf = (int)((c - c_begin) & 1);
+        __syncthreads();  // X tile of chunk c is in xs[buf]
+        x_fetch(c + 1);
+        lkg::raw_load(nxt, W0, r, kb_of(c + 1));
+        if constexpr (SW) lkg::raw_load(nxtu, W1, r, kb_of(c + 1));
+        chunk(c, buf);
+        x_norm(c + 1);
+        x_store(buf ^ 1);  // last read in the previous chunk, before this chunk's barrier
+        cur = nxt;
+        if constexpr (SW) curu = nxtu;
+    }
+    if (c < c_end) {
+        __syncthreads();  // X tile of chunk c is in xs[buf]
+        chunk(c, (int)((c - c_begin) & 1));
     }
     __syncthreads();  // every wave is done with xs: it now holds the output tile(s)
 
