@@ -1672,9 +1672,9 @@ static hipError_t batch_enqueue_single(lkhip_batch* b, hipStream_t st) {
 
 // Fewest rows a step takes on the persistent multi-row step by default: none
 // (LK_BS_MAX_ROWS + 1).  Measured on MI355X at the Qwen2.5-0.5B Q8_0 shape it
-// is slower than the paths it would replace at every row count (4 rows 1.48
-// ms per step against 0.75 on fused_rows_kernel, 16 rows 1.62 against 1.50 on
-// the per-layer launches, 64 rows 2.40 against 2.04): its five grid barriers
+// is slower than the paths it would replace at every row count (4 rows 1.46
+// ms per step against 0.75 on fused_rows_kernel, 16 rows 1.59 against 1.50 on
+// the per-layer launches, 64 rows 2.33 against 2.04): its five grid barriers
 // and split-K round trips per layer cost 8-17 us a phase.
 // LKHIP_BATCH_STEP_MIN=n turns it on from n rows.
 #ifndef LK_BSTEP_MIN_ROWS
