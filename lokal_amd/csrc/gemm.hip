@@ -465,12 +465,9 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, in
     if (n >= a.N) return;
     const bool sw = mode == LK_MV_SWIGLU;
     const size_t np = sw ? 2 * (size_t)a.N : a.N;
-    float v = 0.f, u = 0.f;
-    for (uint32_t z = 0; z < a.ks; z++) {
-        const float* p = a.part + ((size_t)z * a.n_rows + b) * np;
-        v += p[n];
-        if (sw) u += p[a.N + n];
-    }
+    const float* p = a.part + (size_t)b * np + n;
+    const float v = lk_sum_splits(p, (size_t)a.n_rows * np, a.ks);
+    const float u = sw ? lk_sum_splits(p + a.N, (size_t)a.n_rows * np, a.ks) : 0.f;
     emit(a, mode, b, n, v, u);
 }
 

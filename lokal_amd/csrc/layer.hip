@@ -231,10 +231,7 @@ __global__ __launch_bounds__(1024) void rows_accnorm_kernel(float* __restrict__ 
     for (uint32_t i = threadIdx.x; i < n; i += 1024) {
         float v = xr[i];
         if (ks) {
-            float a = 0.f;
-#pragma unroll 8
-            for (uint32_t z = 0; z < ks; z++) a += part[((size_t)z * rows + r) * n + i];
-            v += a;
+            v += lk_sum_splits(part + (size_t)r * n + i, (size_t)rows * n, ks);
             xr[i] = v;
         }
         ss = fmaf(v, v, ss);
@@ -275,8 +272,7 @@ __global__ __launch_bounds__(256) void rows_rope_kv_kernel(float* __restrict__ q
     float* row = qkv + (size_t)r * qkvd;
     auto val = [&](uint32_t idx) -> float {
         if (!ks) return row[idx];
-        float a = 0.f;
-        for (uint32_t z = 0; z < ks; z++) a += part[((size_t)z * rows + r) * qkvd + idx];
+        const float a = lk_sum_splits(part + (size_t)r * qkvd + idx, (size_t)rows * qkvd, ks);
         const float* b = idx < qd ? bq : (idx < qd + kvd ? bk : bv);
         const uint32_t bi = idx < qd ? idx : (idx < qd + kvd ? idx - qd : idx - qd - kvd);
         return b ? a + b[bi] : a;

@@ -27,6 +27,23 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* lk_g(const
     return (const __attribute__((address_space(1))) T*)p;
 }
 
+// Sum of ks split-K partials p[z * stride], z = 0..ks-1, added in split
+// order (bit-identical to the plain loop).  The loads go out 16 at a time
+// (clamped in-range addresses, unused values dropped by a select), so a
+// thread waits one memory round trip per 16 splits, not one per split: a
+// runtime-count loop of dependent adds is issued load by load.
+__device__ __forceinline__ float lk_sum_splits(const float* __restrict__ p, size_t stride, uint32_t ks) {
+    float a = 0.f;
+    for (uint32_t z0 = 0; z0 < ks; z0 += 16) {
+        float t[16];
+#pragma unroll
+        for (uint32_t j = 0; j < 16; j++) t[j] = p[(size_t)(z0 + j < ks ? z0 + j : z0) * stride];
+#pragma unroll
+        for (uint32_t j = 0; j < 16; j++) a = z0 + j < ks ? a + t[j] : a;
+    }
+    return a;
+}
+
 // Wave-64 reductions on the DPP network (no LDS round trips): quad_perm
 // pairs, row_ror 4 / 8 give every lane its 16-lane row total, row_bcast 15 /
 // 31 carry the row totals up to lane 63, whose value is broadcast.
