@@ -76,6 +76,7 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
 // count is the first row's.
 template <int G, int PR = 1>
 __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t nch) {
+    if (nch == 1) return;  // write_chunk_partial wrote the output itself
     __shared__ uint32_t last;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -123,11 +124,15 @@ __device__ __forceinline__ void count_in_and_fold(const LkAttnArgs& a, uint32_t 
 }
 
 // The 4 waves' (m, l, acc) of each head (red_m[w][g] etc.) -> the chunk's
-// partial per head, with coherent stores.
+// partial per head, with coherent stores.  The only chunk of its (sequence,
+// kv head) (nch == 1) writes the output acc / l instead: the fold would
+// weight that one partial by exp(0) = 1 and return the same quotient, so the
+// partial store, the count and the fold's reads are skipped.
 // PR > 1: columns c = (row seq + c / G, head c % G), as in count_in_and_fold.
 template <int G, int PR = 1, typename RM, typename RA>
 __device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_t seq, uint32_t kvh, uint32_t chunk,
-                                                    const RM& red_m, const RM& red_l, const RA& red_acc) {
+                                                    uint32_t nch, const RM& red_m, const RM& red_l,
+                                                    const RA& red_acc) {
     float* const part1 = a.part + (((size_t)seq * a.n_heads + (size_t)kvh * G) * a.cstride + chunk) * (2 + LK_HD);
     for (int t = threadIdx.x; t < G * PR * LK_HD; t += LK_AW * 64) {
         const int g = t / LK_HD, d = t % LK_HD;  // g: the column
@@ -151,6 +156,13 @@ __device__ __forceinline__ void write_chunk_partial(const LkAttnArgs& a, uint32_
                 L = fmaf(sc, red_l[ww][g], L);
                 A = fmaf(sc, red_acc[ww][g][d], A);
             }
+        }
+        if (nch == 1) {
+            // write-through, as the fold's output: read by another XCD later
+            // in the same launch (the persistent Batcher step's o_proj phase)
+            const uint32_t rs = PR == 1 ? seq : seq + (uint32_t)g / G, hg = PR == 1 ? (uint32_t)g : (uint32_t)g % G;
+            st_coherent(a.out + ((size_t)rs * a.n_heads + kvh * G + hg) * LK_HD + d, A / L);
+            continue;
         }
         float* ph = part;
         if (d == 0) {
@@ -349,6 +361,6 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
 #pragma unroll
         for (int i = 0; i < 4; i++) red_acc[w][4 * j + i][4 * c16 + d] = o[d][i];
     __syncthreads();
-    write_chunk_partial<G, PR>(a, seq, kvh, chunk, red_m, red_l, red_acc);
+    write_chunk_partial<G, PR>(a, seq, kvh, chunk, nch, red_m, red_l, red_acc);
     count_in_and_fold<G, PR>(a, seq, kvh, nch);
 }

@@ -253,6 +253,22 @@ def test_attention_chunk_plans():
 
 
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_attention_one_chunk_per_pair(kernel, monkeypatch):
+    """64 or more (sequence, kv head) pairs over a cache of at most 1024
+    positions take one chunk each, whose block writes the output without the
+    partial / count / fold round trip: ragged contexts from 1 to 1024 (one
+    and two tiles per wave), 4 kv heads, and 1025 positions (the chunked plan
+    again), on both f16 kernels, repeated on the same scratch buffer."""
+    monkeypatch.setenv("LKHIP_ATTN", kernel)
+    rng = np.random.default_rng(61)
+    ctx32 = [1, 2, 63, 64, 65, 511, 512, 513, 1023, 1024] + [int(c) for c in rng.integers(1, 1025, 22)]
+    _attn_case(32, 14, 2, ctx32, 1024, seed=61)
+    _attn_case(40, 32, 4, [int(c) for c in rng.integers(1, 513, 40)], 512, seed=62)
+    _attn_case(32, 14, 2, [1025] + ctx32[1:], 1025, seed=63)
+    _attn_case(32, 14, 2, ctx32, 1024, seed=61)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
 def test_attention_both_f16_kernels(kernel, monkeypatch):
     """The vector-ALU and matrix-core partial kernels (the matrix-core one by
     default, LKHIP_ATTN=valu selects the other) on the same cases, short and long."""
