@@ -282,9 +282,9 @@ __global__ __launch_bounds__(LK_AW * 64) void attn_partial_kernel(const LkAttnAr
 //            disjoint LDS banks.
 // At GQA 7 this is ~1/5 of the vector-ALU work of the scalar kernel, whose
 // FMA rate per HBM byte is close to the ALU's.
-template <int G, int PR>
+template <int G, int PR, bool ROPE = false>
 __global__ __launch_bounds__(LK_AW * 64) void attn_mfma_kernel(const LkAttnArgs a) {
-    attn_mfma_item<G, PR>(a, blockIdx.x, blockIdx.y, blockIdx.z * PR);
+    attn_mfma_item<G, PR, ROPE>(a, blockIdx.x, blockIdx.y, blockIdx.z * PR);
 }
 // Rows per item of a grouped (prefill) launch: as many as fill the 16 MFMA columns.
 static constexpr uint32_t attn_rows_per_item(uint32_t G) { return 16 / G; }
@@ -301,6 +301,15 @@ hipError_t lk_attn_launch(const LkAttnArgs& args, hipStream_t st) {
     // a prefill chunk on the matrix-core kernel: several rows per item, so a
     // K/V tile is read once for all of them
     const bool group = a.grouped && !a.kv_f32 && mfma && G <= 8;
+    if (a.rope && (a.kv_f32 || group || !mfma)) {
+        // the RoPE + KV append as its own launch first: only the one-row f16
+        // matrix-core kernel does it in the attention launch
+        const hipError_t e = lk_rows_rope_kv_launch((float*)a.q, a.rope_part, a.rope_ks, a.bq, a.bk, a.bv, a.n_heads,
+                                                    a.n_kv, a.freq, a.pos_rows, a.n_seq, (void*)a.k, (void*)a.v,
+                                                    (int)a.kv_f32, a.max_seq, a.seq_stride, a.slots, st);
+        if (e != hipSuccess) return e;
+        a.rope = 0;
+    }
     const uint32_t pr = group ? attn_rows_per_item(G) : 1;
     const uint32_t items = (a.n_seq + pr - 1) / pr;
     const AttnPlan p = attn_plan(items, a.n_kv, a.max_seq);
@@ -312,6 +321,7 @@ hipError_t lk_attn_launch(const LkAttnArgs& args, hipStream_t st) {
     case g:                                                                                     \
         if (a.kv_f32) hipLaunchKernelGGL((attn_partial_kernel<g, float>), grid, dim3(LK_AW * 64), 0, st, a); \
         else if (group) hipLaunchKernelGGL((attn_mfma_kernel<g, attn_rows_per_item(g)>), grid, dim3(LK_AW * 64), 0, st, a); \
+        else if (mfma && a.rope) hipLaunchKernelGGL((attn_mfma_kernel<g, 1, true>), grid, dim3(LK_AW * 64), 0, st, a); \
         else if (mfma) hipLaunchKernelGGL((attn_mfma_kernel<g, 1>), grid, dim3(LK_AW * 64), 0, st, a);     \
         else hipLaunchKernelGGL((attn_partial_kernel<g, uint16_t>), grid, dim3(LK_AW * 64), 0, st, a);  \
         break;

@@ -192,8 +192,9 @@ __device__ __forceinline__ lk_h4 h4_bits(uint32_t lo, uint32_t hi) {
 // rows' G heads as the MFMA's G * PR <= 16 columns, column c = (row c / G,
 // head c % G), and each K/V tile is read once for all of them; a column's
 // positions past its own row's are masked (causal).
-template <int G, int PR = 1>
+template <int G, int PR = 1, bool ROPE = false>
 __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chunk, uint32_t kvh, uint32_t seq) {
+    static_assert(!ROPE || PR == 1, "RoPE in the attention launch is for one-row items");
     static_assert(G * PR <= 16, "the item's columns fit one 16-column MFMA tile");
     // the item's context: its last row's (positions grow along the rows)
     const uint32_t rlast = PR == 1 ? seq : (seq + PR - 1 < a.n_seq ? seq + PR - 1 : a.n_seq - 1);
@@ -224,6 +225,52 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
     const bool clive = PR == 1 ? c16 < (uint32_t)G : (c16 < (uint32_t)(G * PR) && seq + crow < a.n_seq);
     const uint32_t cctx = PR > 1 ? attn_ctx(a, clive ? seq + crow : seq) : ctx;  // the column's causal bound
 
+    // LkAttnArgs::rope: this row's q heads of kv head kvh rotated into rq, and,
+    // in the block whose chunk holds position plast, the row's k / v (rounded
+    // to f16) into rkh / rvh and the cache
+    __shared__ float rq[ROPE ? G * LK_HD : 1];
+    __shared__ __align__(16) uint16_t rkh[ROPE ? LK_HD : 8], rvh[ROPE ? LK_HD : 8];
+    constexpr bool rope = ROPE;
+    const bool own_pos = ROPE && plast < c0 + CH;  // c0 <= plast: c0 < ctx
+    if constexpr (ROPE) {
+        const uint32_t qd = a.n_heads * LK_HD, kvd = a.n_kv * LK_HD;
+        const float fpos = (float)plast;
+        // element idx of the row's q | k | v: split-K partials summed in
+        // split order, then the bias (rows_rope_kv_kernel's order)
+        auto val = [&](uint32_t idx, const float* bias, uint32_t bi) -> float {
+            if (!a.rope_ks) return a.q[(size_t)seq * a.q_stride + idx];
+            const float sum = lk_sum_splits(a.rope_part + (size_t)seq * a.q_stride + idx,
+                                             (size_t)a.n_seq * a.q_stride, a.rope_ks);
+            return bias ? sum + bias[bi] : sum;
+        };
+        const uint32_t nq = G * 32, nt = nq + (own_pos ? 32 + LK_HD : 0);
+        for (uint32_t t = (uint32_t)tid; t < nt; t += LK_AW * 64) {
+            if (t < nq) {
+                const uint32_t g = t / 32, i = t % 32, o = (kvh * G + g) * LK_HD + i;
+                float x0 = val(o, a.bq, o), x1 = val(o + 32, a.bq, o + 32);
+                lk_rot_pair(x0, x1, __fmul_rn(fpos, a.freq.f[i]));
+                rq[g * LK_HD + i] = x0;
+                rq[g * LK_HD + i + 32] = x1;
+            } else if (t < nq + 32) {
+                const uint32_t i = t - nq, o = kvh * LK_HD + i;
+                float x0 = val(qd + o, a.bk, o), x1 = val(qd + o + 32, a.bk, o + 32);
+                lk_rot_pair(x0, x1, __fmul_rn(fpos, a.freq.f[i]));
+                const uint16_t h0 = __half_as_ushort(__float2half_rn(x0)), h1 = __half_as_ushort(__float2half_rn(x1));
+                rkh[i] = h0;
+                rkh[i + 32] = h1;
+                uint16_t* Kw = (uint16_t*)a.k + kv_base + (size_t)plast * LK_HD;
+                Kw[i] = h0;
+                Kw[i + 32] = h1;
+            } else {
+                const uint32_t d = t - nq - 32, o = kvh * LK_HD + d;
+                const uint16_t hv = __half_as_ushort(__float2half_rn(val(qd + kvd + o, a.bv, o)));
+                rvh[d] = hv;
+                ((uint16_t*)a.v)[kv_base + (size_t)plast * LK_HD + d] = hv;
+            }
+        }
+        __syncthreads();
+    }
+
     // q of column c16 (zero for a dead column), dims 16j + 4s .. +3 for step s, as f16 hi + lo
     lk_h4 qh[4], ql[4];
     {
@@ -232,8 +279,16 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
         for (int st = 0; st < 4; st++) {
             // coherent: q may have been written earlier in the same launch
             // (the persistent Batcher step) by another XCD
-            const float x[4] = {ld_coherent(qrow + 16 * j + 4 * st), ld_coherent(qrow + 16 * j + 4 * st + 1),
-                                ld_coherent(qrow + 16 * j + 4 * st + 2), ld_coherent(qrow + 16 * j + 4 * st + 3)};
+            float x[4];
+            if constexpr (rope) {
+                const float4 r4 = *(const float4*)&rq[cg * LK_HD + 16 * j + 4 * st];
+                x[0] = r4.x, x[1] = r4.y, x[2] = r4.z, x[3] = r4.w;
+            } else {
+                x[0] = ld_coherent(qrow + 16 * j + 4 * st);
+                x[1] = ld_coherent(qrow + 16 * j + 4 * st + 1);
+                x[2] = ld_coherent(qrow + 16 * j + 4 * st + 2);
+                x[3] = ld_coherent(qrow + 16 * j + 4 * st + 3);
+            }
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float xv = clive ? x[e] : 0.f;
@@ -267,6 +322,24 @@ __device__ __forceinline__ void attn_mfma_item(const LkAttnArgs& a, uint32_t chu
         for (int it = 0; it < 8; it++) {
             const uint32_t p = p0 + 8u * it + ((uint32_t)lane >> 3);
             vr[it] = *(const lk_u4*)(V + (size_t)(p < ctx ? p : plast) * LK_HD + 8 * (lane & 7));
+        }
+        if (ROPE && own_pos && plast < p0 + 64) {
+            // this tile holds position plast: its K / V row (and the clamped
+            // rows past it, masked below) from rkh / rvh, not the cache row
+            // this launch is writing
+            const uint4 k0 = *(const uint4*)&rkh[16 * j], k1 = *(const uint4*)&rkh[16 * j + 8];
+            const lk_u4 vv = *(const lk_u4*)&rvh[8 * (lane & 7)];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t p = p0 + 16u * t + 4u * (c16 & 3) + (c16 >> 2);
+                if (p >= plast) {
+                    kr[t][0] = k0;
+                    kr[t][1] = k1;
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < 8; it++)
+                if (p0 + 8u * it + ((uint32_t)lane >> 3) >= plast) vr[it] = vv;
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the previous tile's V reads are done
         __builtin_amdgcn_wave_barrier();

@@ -79,15 +79,6 @@ __device__ __forceinline__ void st1(float* p, float v) {
     __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// RoPE of one pair (src/model.rs:268-279), as the multi-row kernels compute it.
-__device__ __forceinline__ void rot_pair(float& a, float& b, float ang) {
-    const float s = sinf(ang), c = cosf(ang);
-    const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    const float nb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
-    a = na;
-    b = nb;
-}
-
 // Grid barrier without read-modify-write: block b stores the barrier's tag
 // (launch epoch * 256 + barrier index) into its own word bar[b], and every
 // block polls all the words (wave 0, every lane a few) until each carries
@@ -402,8 +393,8 @@ __device__ __forceinline__ void lin_item(const LkBatchStepArgs& a, const Lin& g,
                     w1 += bias[o + 33];
                 }
                 const float fpos = (float)pos;
-                rot_pair(v0, w0, __fmul_rn(fpos, a.freq.f[i]));
-                rot_pair(v1, w1, __fmul_rn(fpos, a.freq.f[i + 1]));
+                lk_rot_pair(v0, w0, __fmul_rn(fpos, a.freq.f[i]));
+                lk_rot_pair(v1, w1, __fmul_rn(fpos, a.freq.f[i + 1]));
                 if (seg == 0) {
                     float* q = a.qkv + (size_t)b * (qd + 2 * kvd) + nh0 + i;
                     st1(q, v0);

@@ -1308,11 +1308,17 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
         }
         uint8_t* kc = kv.kc + L * kv.layer_bytes;
         uint8_t* vc = kv.vc + L * kv.layer_bytes;
-        RSTEP(lk_rows_rope_kv_launch(qkv, part, ks, ly.has_bias ? ly.bq.as<float>() : nullptr,
-                                     ly.has_bias ? ly.bk.as<float>() : nullptr,
-                                     ly.has_bias ? ly.bv.as<float>() : nullptr, c.num_attention_heads,
-                                     c.num_key_value_heads, e->freq, pos, n, kc, vc, kv.kv_f32, kv.kv_seq,
-                                     kv.slot_elems, slots, st));
+        const float* bq = ly.has_bias ? ly.bq.as<float>() : nullptr;
+        const float* bk = ly.has_bias ? ly.bk.as<float>() : nullptr;
+        const float* bv = ly.has_bias ? ly.bv.as<float>() : nullptr;
+        // Batcher rows (sequences that never read each other's K/V): the
+        // attention launch rotates q and appends each row's own k / v itself
+        // (LkAttnArgs::rope).  A prompt chunk's rows read each other's K/V,
+        // so every row is appended first.
+        const bool rope_in_attn = !one_seq && !(head == HEAD_NONE && L + 1 == c.num_hidden_layers);
+        if (!rope_in_attn)
+            RSTEP(lk_rows_rope_kv_launch(qkv, part, ks, bq, bk, bv, c.num_attention_heads, c.num_key_value_heads,
+                                         e->freq, pos, n, kc, vc, kv.kv_f32, kv.kv_seq, kv.slot_elems, slots, st));
         // without logits only the last layer's K/V are needed from it
         if (head == HEAD_NONE && L + 1 == c.num_hidden_layers) break;
         {
@@ -1332,6 +1338,16 @@ static hipError_t enqueue_rows(const lkhip_engine* e, Rows& R, uint32_t n, const
             a.seq_stride = kv.slot_elems;
             a.q_stride = qkvd;
             a.grouped = one_seq ? 1u : 0u;
+            if (rope_in_attn) {
+                a.rope = 1;
+                a.rope_ks = ks;
+                a.rope_part = part;
+                a.bq = bq;
+                a.bk = bk;
+                a.bv = bv;
+                a.pos_rows = pos;
+                a.freq = e->freq;
+            }
             RSTEP(lk_attn_launch(a, st));
         }
         {

@@ -30,16 +30,7 @@ hipError_t lk_rmsnorm_launch(const float* x, const float* w, uint32_t rows, uint
 
 // ------------------------------------------------------------------- RoPE
 // model::rope (src/model.rs:268-279): pair (i, i+hd/2) of each head turns by
-// pos * theta^(-2i/hd).  The inverse frequencies come from the host (same
-// powf as the CPU path), so (float)pos * f is bit-identical and only sinf /
-// cosf can differ.  Products are kept unfused, as the CPU computes them.
-__device__ __forceinline__ void rot_pair(float& a, float& b, float ang) {
-    const float s = sinf(ang), c = cosf(ang);
-    const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    const float nb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
-    a = na;
-    b = nb;
-}
+// pos * theta^(-2i/hd) (lk_rot_pair).
 
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, uint32_t rows, uint32_t n, uint32_t hd,
                                                    const uint32_t* __restrict__ pos, const LkFreq fr) {
@@ -51,7 +42,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, uint32
     const uint32_t head = pr / half, i = pr % half;
     float* hx = x + (size_t)r * n + (size_t)head * hd;
     float a = hx[i], b = hx[i + half];
-    rot_pair(a, b, __fmul_rn((float)pos[r], fr.f[i]));
+    lk_rot_pair(a, b, __fmul_rn((float)pos[r], fr.f[i]));
     hx[i] = a;
     hx[i + half] = b;
 }
@@ -91,14 +82,14 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, u
         const uint32_t head = t / 32, i = t % 32;
         float* h = row + head * 64;
         float a = h[i], b = h[i + 32];
-        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
         h[i] = a;
         h[i + 32] = b;
     } else if (t < nq_pairs + nk_pairs) {
         const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
         float* h = row + qd + head * 64;
         float a = h[i], b = h[i + 32];
-        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
         h[i] = a;
         h[i + 32] = b;
         KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
@@ -284,14 +275,14 @@ __global__ __launch_bounds__(256) void rows_rope_kv_kernel(float* __restrict__ q
         const uint32_t head = t / 32, i = t % 32;
         const uint32_t o = head * 64 + i;
         float a = val(o), b = val(o + 32);
-        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
         row[o] = a;
         row[o + 32] = b;
     } else if (t < nq_pairs + nk_pairs) {
         const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
         const uint32_t o = qd + head * 64 + i;
         float a = val(o), b = val(o + 32);
-        rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
         KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
         kv_store(dst + i, a);
         kv_store(dst + i + 32, b);

@@ -27,6 +27,19 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* lk_g(const
     return (const __attribute__((address_space(1))) T*)p;
 }
 
+// RoPE of one pair (i, i + hd/2) turned by ang = pos * theta^(-2i/hd)
+// (model::rope, src/model.rs:268-279).  The inverse frequencies come from the
+// host (same powf as the CPU path), so pos * f is bit-identical and only
+// sinf / cosf can differ.  Products are kept unfused, as the CPU computes
+// them.  Every multi-row kernel that rotates q or k calls this one.
+__device__ __forceinline__ void lk_rot_pair(float& a, float& b, float ang) {
+    const float s = sinf(ang), c = cosf(ang);
+    const float na = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    const float nb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    a = na;
+    b = nb;
+}
+
 // Sum of ks split-K partials p[z * stride], z = 0..ks-1, added in split
 // order (bit-identical to the plain loop).  The loads go out 16 at a time
 // (clamped in-range addresses, unused values dropped by a select), so a
@@ -269,6 +282,19 @@ struct LkAttnArgs {
     // prefill chunk: one slot, ctx_len[i] + 1 == ctx_len[i + 1]), so an item
     // may take several rows at once (f16 cache, matrix-core kernel)
     uint32_t grouped;
+    // rope != 0 (one row per item): q and each row's own k / v are not rotated
+    // or appended yet.  The launch sums the QKV GEMM's split-K partials
+    // (rope_part, [rope_ks][n_seq][q_stride]; rope_ks == 0: q already holds
+    // the bias-added sums) plus bq / bk / bv, turns q and k by RoPE at the
+    // row's position ctx_len - 1 (= pos_rows), and the block whose chunk holds
+    // that position writes the row's k / v to the cache and uses them -- the
+    // work of rows_rope_kv_kernel, which lk_attn_launch runs first instead
+    // when its kernel for the call is not the one-row f16 matrix-core one.
+    uint32_t rope, rope_ks;
+    const float* rope_part;
+    const float *bq, *bk, *bv;
+    const uint32_t* pos_rows;
+    LkFreq freq;
 };
 uint32_t lk_attn_chunk(uint32_t max_seq);
 // Sets a's chunk plan (waves, tiles, cstride) for its n_seq, n_kv and

@@ -258,3 +258,37 @@ def test_prefill_batcher_and_greedy_match(kind):
         x.close()
     eng.close()
     om.close()
+
+
+@pytest.mark.parametrize("attn", ["mfma", "valu"])
+@pytest.mark.parametrize("kind", ["q4_k_m", "q5_0"])
+def test_batcher_per_layer_step_rope_in_attention(kind, attn, monkeypatch):
+    """Batcher steps of 12 rows (the per-layer launches), where the attention
+    launch rotates q and appends each row's own k / v: on a mixed model whose
+    q/k/v types differ in some layers (per-projection QKV sums, no split-K
+    partials) and on a model with q/k/v biases; with the vector-ALU kernel the
+    RoPE + KV append runs as its own launch first.  Ragged positions, rows
+    out of slot order, three steps, each row against the oracle's sequence."""
+    monkeypatch.setenv("LKHIP_ATTN", attn)
+    cfg, tensors = MODELS[kind](4)
+    eng = Engine.from_tensors(cfg, tensors)
+    om = oracle.Model(cfg, tensors)
+    rng = np.random.default_rng(4)
+    lens = (3, 70, 1, 33, 12, 5, 64, 2, 17, 40, 9, 1)
+    bat = eng.batcher(len(lens), 128)
+    orc = [om.session(128, kv_f16=True) for _ in lens]
+    for slot, n in enumerate(lens):
+        p = rng.integers(0, cfg.vocab_size, n).astype(np.uint32)
+        assert rel_err(bat.prefill(slot, p), orc[slot].prefill(p)) < TOL_F16_KV
+    pos = list(lens)
+    for step in range(3):
+        order = list(rng.permutation(len(lens)))
+        rows = [BatchRow(int(rng.integers(0, cfg.vocab_size)), pos[s], int(s)) for s in order]
+        for r, out in zip(rows, bat.decode_step(rows)):
+            assert rel_err(out, orc[r.slot].forward(r.token, r.pos)) < TOL_F16_KV, (step, r.slot)
+            pos[r.slot] += 1
+    bat.close()
+    for x in orc:
+        x.close()
+    eng.close()
+    om.close()
