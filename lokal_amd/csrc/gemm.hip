@@ -31,6 +31,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 namespace lkg {
 
@@ -459,6 +460,226 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// gemm16_kernel for a wide, shallow matrix (the lm_head: N = vocab rows, K =
+// hidden <= 1024) and a few activation rows: there every one of the N / 64
+// blocks of gemm16_kernel converted the same X tile to its f16 planes
+// again, chunk by chunk.  Here a block (8 waves, one per CU: its X planes
+// take ~120 KB of LDS) converts its 16 * MB rows of X once, whole K, with
+// the same per-(row, chunk) scales, and each wave then streams 16-row weight
+// tiles (every chunk of a tile loaded at once, the next tile's loads issued
+// before the current tile's MFMAs) against the resident planes.  Per chunk
+// the arithmetic is gemm16_kernel's, in the same order, so the results are
+// bit-identical to it.
+constexpr int WIDE_W = 8;  // waves per block
+
+// NCK: the K chunks of a tile, ceil(K / 128) exactly (a compile-time count,
+// so the compiler can count the loads in flight and wait for one chunk at a
+// time)
+template <int WT, int MB, uint32_t NCK>
+__global__ __launch_bounds__(WIDE_W * 64) void gemm16_wide_kernel(const LkGemmArgs a) {
+    constexpr int BR = 16 * MB;
+    extern __shared__ __align__(16) _Float16 wl[];
+    const uint32_t B = a.n_rows, K = a.K, N = a.N;
+    const uint32_t nck = (K + KC - 1) / KC;
+    const uint32_t xs = nck * KC + 8;  // LDS row stride of a plane (halves)
+    _Float16* xh = wl;
+    _Float16* xl = wl + BR * xs;
+    float* xsc = (float*)(xl + BR * xs);  // [BR][NCK]
+    float* sdw = xsc + BR * NCK;     // [WIDE_W][64]: a wave's block scales of one chunk
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t j = (uint32_t)lane >> 4;
+    const uint32_t b0 = blockIdx.y * BR;
+
+    const LkDevW W = a.seg[0].w;
+    const uint32_t ntile = (N + 15) / 16, step = gridDim.x * WIDE_W;
+    Raw16<WT> rw[NCK];
+    auto row_of = [&](uint32_t t) {
+        const uint32_t r = t * 16 + ((uint32_t)lane & 15);
+        return r < N ? r : N - 1;
+    };
+    // X rows b0 .. b0 + BR - 1, every chunk: gemm16_kernel's x_fetch + x_store
+    // (rows past B repeat row B - 1 and are never written out); all of a
+    // thread's loads are issued before any conversion
+    constexpr int XV = BR * KC / 4 / (WIDE_W * 64);
+    float4 xv[NCK][XV];
+#pragma unroll
+    for (uint32_t c = 0; c < NCK; c++)
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + WIDE_W * 64 * i;
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            uint32_t bb = b0 + row;
+            bb = bb < B ? bb : B - 1;
+            const uint32_t k = c * KC + col;
+            const float4 v4 = *(const float4*)(a.x + (size_t)bb * a.ldx + (k < K ? k : 0));
+            xv[c][i] = k < K ? v4 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    {
+        // the wave's first weight tile, in flight during the conversion (a
+        // wave with no tile reloads the last one, unused)
+        const uint32_t t0 = blockIdx.x * WIDE_W + wave;
+        const uint32_t r = row_of(t0 < ntile ? t0 : ntile - 1);
+#pragma unroll
+        for (uint32_t c = 0; c < NCK; c++) raw16_load(rw[c], W, r, c, j, K);
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < NCK; c++)
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint32_t e = threadIdx.x + WIDE_W * 64 * i;
+            const uint32_t row = e / (KC / 4), col = (e % (KC / 4)) * 4;
+            const float4 x4 = xv[c][i];
+            float mx = fmaxf(fmaxf(fabsf(x4.x), fabsf(x4.y)), fmaxf(fabsf(x4.z), fabsf(x4.w)));
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            int ex = 0;
+            (void)frexpf(mx, &ex);
+            const float inv = ldexpf(1.0f, -ex), sc = ldexpf(1.0f, ex);
+            const float v[4] = {x4.x * inv, x4.y * inv, x4.z * inv, x4.w * inv};
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                hi[q] = (_Float16)v[q];
+                lo[q] = (_Float16)(v[q] - (float)hi[q]);
+            }
+            *(uint2*)&xh[row * xs + c * KC + col] = __builtin_bit_cast(uint2, hi);
+            *(uint2*)&xl[row * xs + c * KC + col] = __builtin_bit_cast(uint2, lo);
+            if (col == 0) xsc[row * NCK + c] = sc;
+        }
+    __syncthreads();
+
+    // one segment, no bias (checked by the host): outputs are plain stores, so
+    // no epilogue load waits (vmcnt) for the next tile's weights in flight
+    float* const out = a.seg[0].out;
+    const uint32_t ldy = a.ldy;
+    float* sd = sdw + wave * 64;
+    // one buffer of a tile's chunks: once chunk c is multiplied, its registers
+    // take chunk c of the wave's next tile, so a tile's loads are in flight
+    // while the current tile is computed (a tile's distance ahead, one buffer)
+
+    // tile t; with NEXT, chunk c's registers are reloaded with tile tn's after use
+    auto tile = [&](uint32_t t, auto next, uint32_t tn) {
+        constexpr bool NEXT = decltype(next)::value;
+        const uint32_t rn = row_of(tn);
+        f4 y[MB];
+#pragma unroll
+        for (int m = 0; m < MB; m++) y[m] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t c = 0; c < NCK; c++) {
+            // c < nck always holds (NCK is the chunk count); the uniform branch
+            // keeps each chunk's arithmetic in a block of its own, so the
+            // compiler does not hoist every chunk's X reads at once (they
+            // would spill), while the reload after it stays unconditional
+            if (c < nck) {
+            if constexpr (WT == LK_Q8_0) sd[j * 16 + (lane & 15)] = lk_h2f((uint16_t)rw[c].d);
+            f4 yc[MB];
+#pragma unroll
+            for (int m = 0; m < MB; m++) yc[m] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int blk = 0; blk < 4; blk++) {
+                const h8 wa = raw16_w<WT>(rw[c], blk);
+                float4 dv;
+                if constexpr (WT == LK_Q8_0) dv = *(const float4*)&sd[blk * 16 + 4 * j];
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    const uint32_t xo = (16u * m + ((uint32_t)lane & 15)) * xs + c * KC + 32 * blk + 8 * j;
+                    const h8 bh = *(const h8*)&xh[xo];
+                    const h8 bl = *(const h8*)&xl[xo];
+                    if constexpr (WT == LK_Q8_0) {
+                        f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bl, D, 0, 0, 0);
+                        yc[m][0] = fmaf(dv.x, D[0], yc[m][0]);
+                        yc[m][1] = fmaf(dv.y, D[1], yc[m][1]);
+                        yc[m][2] = fmaf(dv.z, D[2], yc[m][2]);
+                        yc[m][3] = fmaf(dv.w, D[3], yc[m][3]);
+                    } else {
+                        yc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, yc[m], 0, 0, 0);
+                        yc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bl, yc[m], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                const float sx = xsc[(16 * m + (lane & 15)) * NCK + c];
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[m][i] = fmaf(sx, yc[m][i], y[m][i]);
+            }
+            }
+            if constexpr (NEXT) raw16_load(rw[c], W, rn, c, j, K);
+        }
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            const uint32_t b = b0 + 16u * m + ((uint32_t)lane & 15);
+            if (b >= B) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t n = t * 16 + 4 * j + i;
+                if (n < N) out[(size_t)b * ldy + n] = y[m][i];
+            }
+        }
+    };
+    uint32_t t = blockIdx.x * WIDE_W + wave;
+    if (t >= ntile) return;  // uniform over the wave; no block barrier follows
+    for (; t + step < ntile; t += step) tile(t, std::true_type{}, t + step);
+    tile(t, std::false_type{}, t);
+}
+
+static size_t wide_lds(int mb, uint32_t nck_hold, uint32_t K) {
+    const uint32_t nck = (K + KC - 1) / KC;
+    return (size_t)2 * 16 * mb * (nck * KC + 8) * sizeof(_Float16) + 16 * mb * nck_hold * 4 + WIDE_W * 64 * 4;
+}
+
+constexpr int WIDE_MAX_DEV = 64;
+
+template <int WT, int MB, uint32_t NCK>
+static hipError_t launch_wide_t(const LkGemmArgs& a, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= WIDE_MAX_DEV) return hipErrorInvalidDevice;
+    // per device: its CU count, and the kernel's dynamic LDS limit raised once
+    // (to the largest K this kernel takes)
+    static int cus[WIDE_MAX_DEV], ready[WIDE_MAX_DEV];
+    if (!ready[dev]) {
+        e = hipFuncSetAttribute((const void*)gemm16_wide_kernel<WT, MB, NCK>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide_lds(MB, NCK, NCK * KC));
+        if (e != hipSuccess) return e;
+        e = hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        ready[dev] = 1;
+    }
+    const dim3 grid((unsigned)cus[dev], (a.n_rows + 16 * MB - 1) / (16 * MB));
+    hipLaunchKernelGGL((gemm16_wide_kernel<WT, MB, NCK>), grid, dim3(WIDE_W * 64), wide_lds(MB, NCK, a.K), st, a);
+    return hipGetLastError();
+}
+
+// The wide kernel's instance for a.K (its chunk count), or
+// hipErrorNotSupported: 4-7 chunks (K 385-896) for Q8_0, 4-5 (K 385-640)
+// for F16 (the lm_head widths of the shipped configs: 896, 576).
+template <int WT, int MB>
+static hipError_t launch_wide_k(const LkGemmArgs& a, hipStream_t st) {
+    switch ((a.K + KC - 1) / KC) {
+    case 4: return launch_wide_t<WT, MB, 4>(a, st);
+    case 5: return launch_wide_t<WT, MB, 5>(a, st);
+    case 6:
+        if constexpr (WT == LK_Q8_0) return launch_wide_t<WT, MB, 6>(a, st);
+        break;
+    case 7:
+        if constexpr (WT == LK_Q8_0) return launch_wide_t<WT, MB, 7>(a, st);
+        break;
+    default: break;
+    }
+    return hipErrorNotSupported;
+}
+static bool wide_k_ok(uint32_t type, uint32_t K) {
+    const char* g = getenv("LKHIP_GEMM_WIDE");  // "0": gemm16_kernel for these shapes too
+    if (g && strcmp(g, "0") == 0) return false;
+    const uint32_t nck = (K + KC - 1) / KC;
+    return nck >= 4 && (type == LK_Q8_0 ? nck <= 7 : (type == LK_F16 ? nck <= 5 : false));
+}
+
 // Sums the K-split partials of element (b, n) in split order, then the epilogue.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, int mode) {
     const uint32_t n = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
@@ -519,6 +740,12 @@ hipError_t launch_t(const LkGemmArgs& a, int mode, uint32_t mb, dim3 grid, hipSt
 
 static uint32_t gemm_mb(uint32_t n_rows) { return n_rows <= 16 ? 1 : 2; }
 
+// Output rows from which a single-segment store GEMM with K <= 1024 takes
+// gemm16_wide_kernel (the lm_head; the layers' matrices are narrower)
+#ifndef LK_GEMM_WIDE_N
+#define LK_GEMM_WIDE_N 16384u
+#endif
+
 LkGemmPlan lk_gemm_plan(uint32_t type, uint32_t N, uint32_t K, uint32_t n_rows, int mode) {
     (void)type;
     LkGemmPlan p{};
@@ -553,6 +780,16 @@ hipError_t lk_gemm_launch(LkGemmArgs a, int mode, hipStream_t st, uint32_t* defe
         for (uint32_t i = 0; i + 1 < a.nseg; i++)
             if (a.seg[i].w.rows % 16) return hipErrorInvalidValue;
     if (a.ldx % 4 || (size_t)(uintptr_t)a.x % 16) return hipErrorInvalidValue;  // float4 X loads
+    // a wide, shallow matrix (the lm_head: one segment, no bias) without a K split: the kernel that
+    // converts X once per block (bit-identical to gemm16_kernel)
+    if (mode == LK_MV_STORE && a.nseg == 1 && !a.seg[0].bias && a.ks <= 1 && a.N >= LK_GEMM_WIDE_N &&
+        lkg::wide_k_ok(type, a.K) && lkg::gemm16_on(type)) {
+        if (deferred_ks) *deferred_ks = 0;
+        a.ks = 1;
+        const bool one = a.n_rows <= 16;
+        if (type == LK_Q8_0) return one ? lkg::launch_wide_k<LK_Q8_0, 1>(a, st) : lkg::launch_wide_k<LK_Q8_0, 2>(a, st);
+        return one ? lkg::launch_wide_k<LK_F16, 1>(a, st) : lkg::launch_wide_k<LK_F16, 2>(a, st);
+    }
     const LkGemmPlan p = lk_gemm_plan(type, a.N, a.K, a.n_rows, mode);
     if (a.ks == 0) a.ks = p.ks;
     if (a.ks > 1 && !a.part) return hipErrorInvalidValue;

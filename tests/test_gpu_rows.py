@@ -85,6 +85,41 @@ def test_matmul_matches_float64(t, rows, cols, n_rows):
     assert rel_err(y.numpy(), y0 + x.astype(np.float64) @ ref.T) < 1e-5
 
 
+@pytest.mark.parametrize("t,rows,cols", [(synth.Q8_0, 20000, 896), (synth.F16, 16400, 576), (synth.Q8_0, 16400, 512)])
+def test_matmul_wide_lm_head_shapes(t, rows, cols, monkeypatch):
+    """Wide, shallow store GEMMs (the lm_head: >= 16384 rows, K <= 896, no
+    bias) take gemm16_wide_kernel, which converts X once per block: one-hot
+    columns bit-exact, random rows within the float64 bound, an output row
+    stride, and every result bit-identical to gemm16_kernel's
+    (LKHIP_GEMM_WIDE=0), at 1-64 activation rows."""
+    data = synth.gen_weight(t, 9, f"w{rows}x{cols}", rows, cols).data
+    w = K.Weight(t, rows, cols, data)
+    ref = dequant(t, data, rows, cols).astype(np.float64)
+    rng = np.random.default_rng(rows + cols)
+    for n in (1, 5, 16, 17, 40, 64):
+        x = rng.standard_normal((n, cols)).astype(np.float32)
+        hit = rng.integers(0, cols, n)
+        x[: n // 2] = 0.0
+        x[np.arange(n // 2), hit[: n // 2]] = 1.0  # the first half one-hot
+        xd = K.DeviceArray.from_numpy(x)
+        outs = []
+        for wide in ("1", "0"):
+            monkeypatch.setenv("LKHIP_GEMM_WIDE", wide)
+            y = K.DeviceArray((n, rows + 16))
+            y.zero()
+            K.matmul(w, xd, n, y, ldy=rows + 16)
+            outs.append(y.numpy())
+        got, base = outs
+        assert np.array_equal(got, base), n
+        assert not got[:, rows:].any()
+        got = got[:, :rows]
+        for i in range(n // 2):
+            assert np.array_equal(got[i], ref[:, hit[i]].astype(np.float32)), (n, i)
+        want = x.astype(np.float64) @ ref.T
+        scale = np.abs(x).astype(np.float64) @ np.abs(ref).T
+        assert np.max(np.abs(got - want) / (scale + 1e-30)) < 1e-6, n
+
+
 def test_matmul_row_strides():
     t, rows, cols, n = synth.Q8_0, 896, 896, 7
     data = synth.gen_weight(t, 5, "w", rows, cols).data
