@@ -47,7 +47,9 @@ static inline uint32_t attn_chunk_cap(uint32_t max_seq) {
 struct AttnPlan {
     uint32_t waves, tiles, chunks;  // active waves per block, tiles per wave, chunks per (seq, kvh)
 };
+#ifndef LK_ATTN_ONE_PAIRS
 #define LK_ATTN_ONE_PAIRS 64
+#endif
 // The largest A in 8, 4, 2, 1 whose grid has >= LK_ATTN_MINBLOCKS blocks,
 // else the one with the most blocks (the larger A on a tie), with T the
 // fewest tiles per wave that keep the chunks per (seq, kvh) <= LK_MAXCH.
