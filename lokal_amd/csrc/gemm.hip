@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
 
 // ---------------------------------------------------------------------------
 // The same GEMM at the f16 matrix-core rate (v_mfma_f32_16x16x32_f16) with
-// f32-level accuracy, for Q8_0 and F16 weights:
+// f32-level accuracy, for Q8_0, F16 and Q4_K weights:
 //   X      each row of a 128-column chunk is scaled by a power of two s (its
 //          largest |x| brought into [0.5, 1)) and split into f16 hi + lo
 //          (x/s = hi + lo to ~22 significant bits; the scaling is exact),
@@ -220,8 +220,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const LkGemmArgs a) {
 //          weights 8j..8j+7 of the block of row m (int8 -> f16 exactly: the
 //          byte biased by 128 is the low mantissa byte of 1024 + q + 128, a
 //          packed subtraction removes the bias); F16 weights as they are;
+//          Q4_K: one MFMA per 32-column sub-block, a nibble n as the f16
+//          1024 + n minus 1024 (exact);
 //   sums   D = W (hi + lo) per block in f32, then y_chunk += d * D with the
-//          block's scale d (Q8_0), and y += s * y_chunk per chunk.
+//          block's scale d (Q8_0; Q4_K: d1 = d * sc, then y_chunk -= m1 *
+//          sum(x/s) over the sub-block, m1 = dmin * m, the sums taken while X
+//          is staged), and y += s * y_chunk per chunk.  A one-hot x still
+//          returns d1 * q - m1 rounded as dequant_row_ref rounds it.
 // The products q * (hi or lo) are exact in f32, so the result differs from
 // the f32 kernel's only by the split's ~2^-22 and the summation order.
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -231,22 +236,36 @@ constexpr uint32_t HS = KC + 8;  // LDS row stride of an f16 plane (halves)
 template <int WT> struct Raw16;
 template <> struct Raw16<LK_Q8_0> { uint2 q[4]; uint32_t d; };
 template <> struct Raw16<LK_F16> { uint4 q[4]; };
+// Q4_K: q[p] = bytes 8j..8j+7 of sub-block pair p of the chunk (low nibbles:
+// sub-block 2p, high nibbles: 2p + 1, columns 8j..8j+7 of each); hd = the
+// row's 16-byte super-block head (d, dmin, 12 packed scale bytes)
+template <> struct Raw16<LK_Q4_K> { uint2 q[2]; uint4 hd; };
 
 // Lane (j, m = row r) of chunk c: weights 8j..8j+7 of each of the chunk's four
 // 32-column blocks of row r; Q8_0 also the scale of row r, block 4c + j.
 template <int WT>
 __device__ __forceinline__ void raw16_load(Raw16<WT>& R, const LkDevW& w, uint32_t r, uint32_t c, uint32_t j,
                                            uint32_t K) {
+    if constexpr (WT == LK_Q4_K) {
+        // chunk c = half c & 1 of super-block c >> 1 (K is a multiple of 256,
+        // so every chunk is whole); 128 qs bytes and a 16-byte head per super-block
+        const uint32_t nsb = w.cols / 256, sbk = c >> 1;
+        const uint8_t* qs = w.data + ((size_t)r * nsb + sbk) * 128 + (c & 1) * 64 + 8 * j;
+        R.q[0] = *(const uint2*)qs;
+        R.q[1] = *(const uint2*)(qs + 32);
+        R.hd = *(const uint4*)(w.aux + ((size_t)r * nsb + sbk) * 16);
+    } else {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) {
-        uint32_t col = c * KC + 32 * blk + 8 * j;
-        col = col < K ? col : 0;  // past K: any in-row weights, multiplied by X = 0
-        if constexpr (WT == LK_Q8_0) R.q[blk] = *(const uint2*)(w.data + (size_t)r * w.cols + col);
-        else R.q[blk] = *(const uint4*)(w.data + ((size_t)r * w.cols + col) * 2);
-    }
-    if constexpr (WT == LK_Q8_0) {
-        const uint32_t b = c * 4 + j;
-        R.d = ((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + (b < K / 32 ? b : 0)];
+        for (int blk = 0; blk < 4; blk++) {
+            uint32_t col = c * KC + 32 * blk + 8 * j;
+            col = col < K ? col : 0;  // past K: any in-row weights, multiplied by X = 0
+            if constexpr (WT == LK_Q8_0) R.q[blk] = *(const uint2*)(w.data + (size_t)r * w.cols + col);
+            else R.q[blk] = *(const uint4*)(w.data + ((size_t)r * w.cols + col) * 2);
+        }
+        if constexpr (WT == LK_Q8_0) {
+            const uint32_t b = c * 4 + j;
+            R.d = ((const uint16_t*)w.aux)[(size_t)r * (w.cols / 32) + (b < K / 32 ? b : 0)];
+        }
     }
 }
 
@@ -255,6 +274,20 @@ template <int WT>
 __device__ __forceinline__ h8 raw16_w(const Raw16<WT>& R, int blk) {
     if constexpr (WT == LK_F16) {
         return __builtin_bit_cast(h8, R.q[blk]);
+    } else if constexpr (WT == LK_Q4_K) {
+        // sub-block blk of the chunk: nibbles n -> the f16 1024 + n (bytes
+        // [n, 0x64]), minus 1024: exact
+        const hh2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const uint2 v = R.q[blk >> 1];
+        const uint32_t sh = (blk & 1) ? 4u : 0u;
+        const uint32_t w0 = (v.x >> sh) & 0x0F0F0F0Fu, w1 = (v.y >> sh) & 0x0F0F0F0Fu;
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+        const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+        const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+        const hh2 q0 = __builtin_bit_cast(hh2, p0) - bias, q1 = __builtin_bit_cast(hh2, p1) - bias;
+        const hh2 q2 = __builtin_bit_cast(hh2, p2) - bias, q3 = __builtin_bit_cast(hh2, p3) - bias;
+        return h8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
     } else {
         const hh2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
         const uint32_t w0 = R.q[blk].x ^ 0x80808080u, w1 = R.q[blk].y ^ 0x80808080u;
@@ -277,6 +310,11 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
     __shared__ __align__(16) _Float16 xh[2][BR * HS], xl[2][BR * HS];
     __shared__ float xsc[2][BR];
     __shared__ __align__(16) float sd[4][NW][64];  // per wave: the chunk's block scales, [block][row]
+    // Q4_K: per wave the chunk's sub-block mins m1 = dmin * m, [block][row]; and
+    // per X buffer the sums of each row's scaled values over every 32-column
+    // sub-block (the min term is m1 * sum(x) per sub-block)
+    __shared__ __align__(16) float sm[WT == LK_Q4_K ? 4 : 1][NW][64];
+    __shared__ float xsum[WT == LK_Q4_K ? 2 : 1][BR][4];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t n0 = (blockIdx.x * 4 + wave) * 16;
@@ -338,6 +376,14 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
             *(uint2*)&xh[buf][row * HS + col] = __builtin_bit_cast(uint2, hi);
             *(uint2*)&xl[buf][row * HS + col] = __builtin_bit_cast(uint2, lo);
             if (col == 0) xsc[buf][row] = sc;
+            if constexpr (WT == LK_Q4_K) {
+                // the sub-block's 8 float4s sit in 8 adjacent lanes
+                float t = (v[0] + v[1]) + (v[2] + v[3]);
+                t += __shfl_xor(t, 1, 64);
+                t += __shfl_xor(t, 2, 64);
+                t += __shfl_xor(t, 4, 64);
+                if (col % 32 == 0) xsum[buf][row][col / 32] = t;
+            }
         }
     };
 
@@ -361,6 +407,19 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
             if constexpr (WT == LK_Q8_0) {  // the chunk's block scales: row lane & 15, block j
                 sd[wave][0][j * 16 + (lane & 15)] = lk_h2f((uint16_t)cur.d);
                 if constexpr (SW) sd[wave][NW - 1][j * 16 + (lane & 15)] = lk_h2f((uint16_t)curu.d);
+            } else if constexpr (WT == LK_Q4_K) {
+                // sub-block j of the chunk (j + 4 (c & 1) of its super-block):
+                // d1 = d * sc and m1 = dmin * m, each rounded once, as
+                // dequant_row_ref does (src/gguf/dequant.rs:462-483)
+                auto put = [&](const Raw16<WT>& R, int sw) {
+                    uint32_t sc, mn;
+                    lk::scale_min_k4((c & 1) * 4 + j, R.hd.y, R.hd.z, R.hd.w, sc, mn);
+                    const float d = lk_h2f((uint16_t)(R.hd.x & 0xFFFF)), dmin = lk_h2f((uint16_t)(R.hd.x >> 16));
+                    sd[wave][sw][j * 16 + (lane & 15)] = __fmul_rn(d, (float)sc);
+                    sm[wave][sw][j * 16 + (lane & 15)] = __fmul_rn(dmin, (float)mn);
+                };
+                put(cur, 0);
+                if constexpr (SW) put(curu, NW - 1);
             }
             f4 yc[MB], ycu[SW ? MB : 1];
 #pragma unroll
@@ -373,23 +432,35 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
                 const h8 wa = raw16_w<WT>(cur, blk);
                 h8 wu;
                 if constexpr (SW) wu = raw16_w<WT>(curu, blk);
-                float4 dv, du;
-                if constexpr (WT == LK_Q8_0) {
+                float4 dv, du, mv, mu;
+                if constexpr (WT == LK_Q8_0 || WT == LK_Q4_K) {
                     dv = *(const float4*)&sd[wave][0][blk * 16 + 4 * j];  // rows 4j..4j+3 of the D layout
                     if constexpr (SW) du = *(const float4*)&sd[wave][NW - 1][blk * 16 + 4 * j];
+                }
+                if constexpr (WT == LK_Q4_K) {
+                    mv = *(const float4*)&sm[wave][0][blk * 16 + 4 * j];
+                    if constexpr (SW) mu = *(const float4*)&sm[wave][NW - 1][blk * 16 + 4 * j];
                 }
 #pragma unroll
                 for (int m = 0; m < MB; m++) {
                     const uint32_t xo = (16u * m + ((uint32_t)lane & 15)) * HS + 32 * blk + 8 * j;
                     const h8 bh = *(const h8*)&xh[buf][xo];
                     const h8 bl = *(const h8*)&xl[buf][xo];
-                    if constexpr (WT == LK_Q8_0) {
+                    if constexpr (WT == LK_Q8_0 || WT == LK_Q4_K) {
                         f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                         D = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bl, D, 0, 0, 0);
                         yc[m][0] = fmaf(dv.x, D[0], yc[m][0]);
                         yc[m][1] = fmaf(dv.y, D[1], yc[m][1]);
                         yc[m][2] = fmaf(dv.z, D[2], yc[m][2]);
                         yc[m][3] = fmaf(dv.w, D[3], yc[m][3]);
+                        float xs = 0.f;
+                        if constexpr (WT == LK_Q4_K) {  // minus m1 * sum(x) of the sub-block
+                            xs = xsum[buf][16 * m + (lane & 15)][blk];
+                            yc[m][0] = fmaf(-mv.x, xs, yc[m][0]);
+                            yc[m][1] = fmaf(-mv.y, xs, yc[m][1]);
+                            yc[m][2] = fmaf(-mv.z, xs, yc[m][2]);
+                            yc[m][3] = fmaf(-mv.w, xs, yc[m][3]);
+                        }
                         if constexpr (SW) {
                             f4 E = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bh, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                             E = __builtin_amdgcn_mfma_f32_16x16x32_f16(wu, bl, E, 0, 0, 0);
@@ -397,6 +468,12 @@ __global__ __launch_bounds__(256) void gemm16_kernel(const LkGemmArgs a) {
                             ycu[m][1] = fmaf(du.y, E[1], ycu[m][1]);
                             ycu[m][2] = fmaf(du.z, E[2], ycu[m][2]);
                             ycu[m][3] = fmaf(du.w, E[3], ycu[m][3]);
+                            if constexpr (WT == LK_Q4_K) {
+                                ycu[m][0] = fmaf(-mu.x, xs, ycu[m][0]);
+                                ycu[m][1] = fmaf(-mu.y, xs, ycu[m][1]);
+                                ycu[m][2] = fmaf(-mu.z, xs, ycu[m][2]);
+                                ycu[m][3] = fmaf(-mu.w, xs, ycu[m][3]);
+                            }
                         }
                     } else {
                         yc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bh, yc[m], 0, 0, 0);
@@ -692,9 +769,9 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const LkGemmArgs a, in
     emit(a, mode, b, n, v, u);
 }
 
-// The f16-rate kernel for Q8_0 and F16 (LKHIP_GEMM=f32 keeps the f32 one).
+// The f16-rate kernel for Q8_0, F16 and Q4_K (LKHIP_GEMM=f32 keeps the f32 one).
 static bool gemm16_on(uint32_t type) {
-    if (type != LK_Q8_0 && type != LK_F16) return false;
+    if (type != LK_Q8_0 && type != LK_F16 && type != LK_Q4_K) return false;
     static int on = -1;
     if (on < 0) {
         const char* g = getenv("LKHIP_GEMM");
@@ -705,7 +782,7 @@ static bool gemm16_on(uint32_t type) {
 
 template <int WT, int MB>
 hipError_t launch_mb16(const LkGemmArgs& a, int mode, dim3 grid, hipStream_t st) {
-    if constexpr (WT == LK_Q8_0 || WT == LK_F16) {
+    if constexpr (WT == LK_Q8_0 || WT == LK_F16 || WT == LK_Q4_K) {
         switch (mode) {
         case LK_MV_STORE: hipLaunchKernelGGL((gemm16_kernel<WT, MB, LK_MV_STORE>), grid, dim3(256), 0, st, a); break;
         case LK_MV_ACC: hipLaunchKernelGGL((gemm16_kernel<WT, MB, LK_MV_ACC>), grid, dim3(256), 0, st, a); break;
