@@ -32,8 +32,21 @@ hipError_t lk_rmsnorm_launch(const float* x, const float* w, uint32_t rows, uint
 // model::rope (src/model.rs:268-279): pair (i, i+hd/2) of each head turns by
 // pos * theta^(-2i/hd) (lk_rot_pair).
 
+// The inverse frequencies of a by-value LkFreq, copied into LDS with
+// compile-time indices.  Indexed by a lane-varying i as a kernel argument,
+// the table made the compiler copy the whole struct into every thread's
+// scratch at kernel entry (~40 MB of scratch writes per launch at 512 rows).
+// Call before any early return: it ends with a block barrier.
+#define LK_FREQ_TO_LDS(fr, fs)                                \
+    __shared__ float fs[64];                                  \
+    if (threadIdx.x == 0) {                                   \
+        _Pragma("unroll") for (int k_ = 0; k_ < 64; k_++) fs[k_] = (fr).f[k_]; \
+    }                                                         \
+    __syncthreads()
+
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, uint32_t rows, uint32_t n, uint32_t hd,
                                                    const uint32_t* __restrict__ pos, const LkFreq fr) {
+    LK_FREQ_TO_LDS(fr, fs);
     const uint32_t half = hd / 2;
     const uint32_t pairs_per_row = n / 2;
     const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -42,7 +55,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, uint32
     const uint32_t head = pr / half, i = pr % half;
     float* hx = x + (size_t)r * n + (size_t)head * hd;
     float a = hx[i], b = hx[i + half];
-    lk_rot_pair(a, b, __fmul_rn((float)pos[r], fr.f[i]));
+    lk_rot_pair(a, b, __fmul_rn((float)pos[r], fs[i]));
     hx[i] = a;
     hx[i + half] = b;
 }
@@ -70,6 +83,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, u
                                                       KV* __restrict__ kc, KV* __restrict__ vc,
                                                       uint32_t max_seq, uint64_t slot_stride,
                                                       const uint32_t* __restrict__ slots) {
+    LK_FREQ_TO_LDS(fr, fs);
     const uint32_t r = blockIdx.y;
     const uint32_t pos = pos_rows ? pos_rows[r] : st->pos;
     const uint32_t slot = slots ? slots[r] : r;
@@ -82,14 +96,14 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, u
         const uint32_t head = t / 32, i = t % 32;
         float* h = row + head * 64;
         float a = h[i], b = h[i + 32];
-        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fs[i]));
         h[i] = a;
         h[i + 32] = b;
     } else if (t < nq_pairs + nk_pairs) {
         const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
         float* h = row + qd + head * 64;
         float a = h[i], b = h[i + 32];
-        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        lk_rot_pair(a, b, __fmul_rn(fpos, fs[i]));
         h[i] = a;
         h[i + 32] = b;
         KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
@@ -256,16 +270,18 @@ __global__ __launch_bounds__(256) void rows_rope_kv_kernel(float* __restrict__ q
                                                            KV* __restrict__ kc, KV* __restrict__ vc,
                                                            uint32_t max_seq, uint64_t slot_stride,
                                                            const uint32_t* __restrict__ slots) {
+    LK_FREQ_TO_LDS(fr, fs);
     const uint32_t r = blockIdx.y;
     const uint32_t pos = pos_rows[r];
     const uint32_t slot = slots[r];
     const uint32_t qd = n_heads * 64, kvd = n_kv * 64, qkvd = qd + 2 * kvd;
     float* row = qkv + (size_t)r * qkvd;
-    auto val = [&](uint32_t idx) -> float {
+    // element idx of the row, with bias b[bi] (the caller names q, k or v's
+    // bias: a select between the three pointers had become a lookup table in
+    // scratch, and by-reference captures had put the arguments there too)
+    auto val = [=](uint32_t idx, const float* b, uint32_t bi) -> float {
         if (!ks) return row[idx];
         const float a = lk_sum_splits(part + (size_t)r * qkvd + idx, (size_t)rows * qkvd, ks);
-        const float* b = idx < qd ? bq : (idx < qd + kvd ? bk : bv);
-        const uint32_t bi = idx < qd ? idx : (idx < qd + kvd ? idx - qd : idx - qd - kvd);
         return b ? a + b[bi] : a;
     };
     const uint32_t t = blockIdx.x * 256 + threadIdx.x;
@@ -274,21 +290,21 @@ __global__ __launch_bounds__(256) void rows_rope_kv_kernel(float* __restrict__ q
     if (t < nq_pairs) {
         const uint32_t head = t / 32, i = t % 32;
         const uint32_t o = head * 64 + i;
-        float a = val(o), b = val(o + 32);
-        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        float a = val(o, bq, o), b = val(o + 32, bq, o + 32);
+        lk_rot_pair(a, b, __fmul_rn(fpos, fs[i]));
         row[o] = a;
         row[o + 32] = b;
     } else if (t < nq_pairs + nk_pairs) {
         const uint32_t u = t - nq_pairs, head = u / 32, i = u % 32;
         const uint32_t o = qd + head * 64 + i;
-        float a = val(o), b = val(o + 32);
-        lk_rot_pair(a, b, __fmul_rn(fpos, fr.f[i]));
+        float a = val(o, bk, o - qd), b = val(o + 32, bk, o - qd + 32);
+        lk_rot_pair(a, b, __fmul_rn(fpos, fs[i]));
         KV* dst = kc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64;
         kv_store(dst + i, a);
         kv_store(dst + i + 32, b);
     } else if (t < nq_pairs + nk_pairs + kvd) {
         const uint32_t u = t - nq_pairs - nk_pairs, head = u / 64, d = u % 64;
-        kv_store(vc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d, val(qd + kvd + u));
+        kv_store(vc + (size_t)slot * slot_stride + ((size_t)head * max_seq + pos) * 64 + d, val(qd + kvd + u, bv, u));
     }
 }
 

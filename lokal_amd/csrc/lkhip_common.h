@@ -41,20 +41,29 @@ __device__ __forceinline__ void lk_rot_pair(float& a, float& b, float ang) {
 }
 
 // Sum of ks split-K partials p[z * stride], z = 0..ks-1, added in split
-// order (bit-identical to the plain loop).  The loads go out 16 at a time
+// order (bit-identical to the plain loop).  The loads go out W at a time
 // (clamped in-range addresses, unused values dropped by a select), so a
-// thread waits one memory round trip per 16 splits, not one per split: a
-// runtime-count loop of dependent adds is issued load by load.
-__device__ __forceinline__ float lk_sum_splits(const float* __restrict__ p, size_t stride, uint32_t ks) {
+// thread waits one memory round trip per W splits, not one per split (a
+// runtime-count loop of dependent adds is issued load by load); W is the
+// smallest of 2, 4, 8, 16 that covers ks (a uniform branch), so few splits
+// do not issue 16 loads each.
+template <int W>
+__device__ __forceinline__ float lk_sum_splits_w(const float* __restrict__ p, size_t stride, uint32_t ks) {
     float a = 0.f;
-    for (uint32_t z0 = 0; z0 < ks; z0 += 16) {
-        float t[16];
+    for (uint32_t z0 = 0; z0 < ks; z0 += W) {
+        float t[W];
 #pragma unroll
-        for (uint32_t j = 0; j < 16; j++) t[j] = p[(size_t)(z0 + j < ks ? z0 + j : z0) * stride];
+        for (uint32_t j = 0; j < W; j++) t[j] = p[(size_t)(z0 + j < ks ? z0 + j : z0) * stride];
 #pragma unroll
-        for (uint32_t j = 0; j < 16; j++) a = z0 + j < ks ? a + t[j] : a;
+        for (uint32_t j = 0; j < W; j++) a = z0 + j < ks ? a + t[j] : a;
     }
     return a;
+}
+__device__ __forceinline__ float lk_sum_splits(const float* __restrict__ p, size_t stride, uint32_t ks) {
+    if (ks <= 2) return lk_sum_splits_w<2>(p, stride, ks);
+    if (ks <= 4) return lk_sum_splits_w<4>(p, stride, ks);
+    if (ks <= 8) return lk_sum_splits_w<8>(p, stride, ks);
+    return lk_sum_splits_w<16>(p, stride, ks);
 }
 
 // Wave-64 reductions on the DPP network (no LDS round trips): quad_perm
