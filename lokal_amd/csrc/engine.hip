@@ -1562,6 +1562,11 @@ struct lkhip_batch {
     size_t single_lds = 0;
     uint32_t single_chunks = 0;
     DevBuf sxb, sqb, spb, sab, sxpb, sib, sepoch, sxcd;
+    // its final norm + lm_head: lm_head_kernel (the session's one-launch head)
+    // in its deferred mode, whose block keys go to hkeys unread (the greedy
+    // fold reads the logits)
+    DevBuf hkeys, hepoch;
+    uint32_t head_blocks = 0;
     std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
     // the persistent multi-row step (batch_step.hip) for bstep_min..64 rows
     bool bstep_ok = false;
@@ -1826,6 +1831,28 @@ static int batch_path(const lkhip_batch* b, const std::vector<size_t>& last_pos)
     return batch_fused_fits(b, last_pos) ? PATH_FUSED : PATH_LAYERS;
 }
 
+// The final norm and lm_head of a one-row step (the row's final x, written by
+// the single-row one-kernel step, in rows.x) into rows.logits: one
+// lm_head_kernel launch in its deferred mode, instead of the norm launch and
+// the GEMM's 16-row tile for one row.
+static hipError_t batch_head_single(lkhip_batch* b, hipStream_t st) {
+    const lkhip_engine* e = b->e;
+    LkHeadArgs a{};
+    a.x = b->rows.x.as<float>();
+    a.x_stride = 1;
+    a.norm = e->norm.as<float>();
+    a.eps = e->cfg.rms_norm_eps;
+    a.w = e->lm_head->dw;
+    a.h = e->cfg.hidden_size;
+    a.vocab = e->cfg.vocab_size;
+    a.logits = b->rows.logits.as<float>();
+    a.keys = b->hkeys.as<uint64_t>();
+    a.epoch = b->hepoch.as<uint32_t>();
+    a.err = b->ferr.as<uint32_t>();
+    a.defer = 1;
+    return lk_lm_head_launch(a, b->head_blocks, st);
+}
+
 // Enqueues a decode step of n rows (meta on the device); greedy adds the
 // argmax feedback.  Replays a captured graph when graphs are on.  fused: the
 // multi-row one-kernel step instead of the per-layer launches.
@@ -1840,7 +1867,8 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, int path 
         else if (path == PATH_FUSED) err = n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st);
         else err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st, false);
         if (err == hipSuccess && path != PATH_LAYERS)
-            err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
+            err = path == PATH_FUSED && n == 1 && b->single_ok ? batch_head_single(b, st)
+                                                               : enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
         if (err != hipSuccess || !greedy) return err;
         return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
                                       b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
@@ -1944,8 +1972,11 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
             (rc = dev_alloc(b->spb, 2 * (size_t)c.num_attention_heads * b->single_chunks * 66 * 8)) ||
             (rc = dev_alloc(b->sab, 2 * (size_t)e->qd * 8 * LK_FUSED_REP)) ||
             (rc = dev_alloc(b->sxpb, 2 * h * 8 * LK_FUSED_REP)) || (rc = dev_alloc(b->sib, 2 * I * 8)) ||
-            (rc = dev_alloc(b->sepoch, 4)) || (rc = dev_alloc(b->sxcd, LK_XCDS * LK_XCD_CNT_STRIDE * 4)))
+            (rc = dev_alloc(b->sepoch, 4)) || (rc = dev_alloc(b->sxcd, LK_XCDS * LK_XCD_CNT_STRIDE * 4)) ||
+            (rc = dev_alloc(b->hkeys, (size_t)LK_HEAD_MAX_BLOCKS * 2 * 8)) || (rc = dev_alloc(b->hepoch, 4)))
             return rc;
+        HIP_OR_FAIL(hipMemset(b->hepoch.p, 0, 4));
+        b->head_blocks = lk_lm_head_blocks(c.vocab_size, e->lm_head->dw.type, c.hidden_size);
         if (!b->ferr.p && (rc = dev_alloc(b->ferr, 4))) return rc;
         HIP_OR_FAIL(hipMemset(b->sxcd.p, 0, LK_XCDS * LK_XCD_CNT_STRIDE * 4));
         HIP_OR_FAIL(hipMemset(b->ferr.p, 0, 4));
