@@ -542,7 +542,7 @@ __global__ __launch_bounds__(BTH, 1) void batch_step_kernel(const LkBatchStepArg
             const uint32_t nch = at.tiles ? (a.kv_seq + 64 * at.waves * at.tiles - 1) / (64 * at.waves * at.tiles) : 1;
             const uint32_t items = nch * a.nkv * B;
             for (uint32_t it = blockIdx.x; it < items; it += gridDim.x)
-                attn_mfma_item<G>(at, it % nch, (it / nch) % a.nkv, it / (nch * a.nkv));
+                attn_mfma_item<G, 1, false, true>(at, it % nch, (it / nch) % a.nkv, it / (nch * a.nkv));
         }
         grid_sync(a, tag0 + 2 + 5 * L + 1, 2 + 5 * L + 1);
         {  // o_proj + residual
