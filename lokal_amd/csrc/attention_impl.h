@@ -45,7 +45,7 @@ __device__ __forceinline__ void st_coherent(float* p, float v) {
 }
 // The attention output: write-through (COH) where a later phase of the same
 // launch reads it on another XCD (the persistent Batcher step), else a plain
-// store -- agent-scope atomic loads and stores cost 13-18% per standalone
+// store -- agent-scope atomic loads and stores cost 8-16% per standalone
 // launch (4 sequences x 24 layers at 4096-32768 positions, measured).
 template <bool COH>
 __device__ __forceinline__ void st_out(float* p, float v) {
