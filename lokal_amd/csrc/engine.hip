@@ -1567,6 +1567,10 @@ struct lkhip_batch {
     // fold reads the logits)
     DevBuf hkeys, hepoch;
     uint32_t head_blocks = 0;
+    // 2-row one-kernel steps: the final norm + lm_head of both rows as one
+    // lm_head_rows_kernel launch instead of the norm launch and the GEMM
+    // (LKHIP_HEAD_ROWS=0 keeps the GEMM)
+    bool head_rows = false;
     std::vector<hipGraphExec_t> fused_graph[2];  // [greedy] by row count
     // the persistent multi-row step (batch_step.hip) for bstep_min..64 rows
     bool bstep_ok = false;
@@ -1853,6 +1857,26 @@ static hipError_t batch_head_single(lkhip_batch* b, hipStream_t st) {
     return lk_lm_head_launch(a, b->head_blocks, st);
 }
 
+// The final norm and lm_head of a 2-row one-kernel step (the rows' final x
+// in rows.x) into rows.logits: one lm_head_rows_kernel launch.
+static bool batch_head_rows_ok(const lkhip_batch* b, uint32_t n) {
+    const lkhip_engine* e = b->e;
+    return b->head_rows && n >= 2 && lk_lm_head_rows_fits(e->lm_head->dw.type, e->cfg.hidden_size, n);
+}
+static hipError_t batch_head_rows(lkhip_batch* b, uint32_t n, hipStream_t st) {
+    const lkhip_engine* e = b->e;
+    LkHeadArgs a{};
+    a.x = b->rows.x.as<float>();
+    a.x_stride = 1;
+    a.norm = e->norm.as<float>();
+    a.eps = e->cfg.rms_norm_eps;
+    a.w = e->lm_head->dw;
+    a.h = e->cfg.hidden_size;
+    a.vocab = e->cfg.vocab_size;
+    a.logits = b->rows.logits.as<float>();
+    return lk_lm_head_rows_launch(a, n, b->head_blocks, st);
+}
+
 // Enqueues a decode step of n rows (meta on the device); greedy adds the
 // argmax feedback.  Replays a captured graph when graphs are on.  fused: the
 // multi-row one-kernel step instead of the per-layer launches.
@@ -1866,9 +1890,11 @@ static int batch_enqueue_step(lkhip_batch* b, uint32_t n, bool greedy, int path 
         if (path == PATH_BSTEP) err = batch_enqueue_bstep(b, n, st);
         else if (path == PATH_FUSED) err = n == 1 && b->single_ok ? batch_enqueue_single(b, st) : batch_enqueue_fused(b, n, st);
         else err = enqueue_rows(b->e, b->rows, n, b->kv, HEAD_ALL, st, false);
-        if (err == hipSuccess && path != PATH_LAYERS)
-            err = path == PATH_FUSED && n == 1 && b->single_ok ? batch_head_single(b, st)
-                                                               : enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
+        if (err == hipSuccess && path != PATH_LAYERS) {
+            if (path == PATH_FUSED && n == 1 && b->single_ok) err = batch_head_single(b, st);
+            else if (path == PATH_FUSED && batch_head_rows_ok(b, n)) err = batch_head_rows(b, n, st);
+            else err = enqueue_rows_head(b->e, b->rows, n, nullptr, 0, HEAD_ALL, st);
+        }
         if (err != hipSuccess || !greedy) return err;
         return lk_rows_greedy2_launch(b->rows.logits.as<float>(), n, b->e->cfg.vocab_size, b->rows.keys.as<uint64_t>(),
                                       b->rows.meta.as<uint32_t>(), b->rows.cap, b->rows.out_ids.as<uint32_t>(), st);
@@ -1959,6 +1985,11 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         } else {
             (void)hipGetLastError();
         }
+    }
+    {
+        const char* hr = getenv("LKHIP_HEAD_ROWS");
+        b->head_rows = b->fused_ok && !(hr && hr[0] == '0');
+        b->head_blocks = lk_lm_head_blocks(c.vocab_size, e->lm_head->dw.type, c.hidden_size);
     }
     // steps of one row: the single-row one-kernel step, for any cache length
     // it takes (LKHIP_BATCH_FUSED=0 keeps these on the per-layer launches too)

@@ -265,6 +265,12 @@ bool lk_lm_head_fits(uint32_t type, uint32_t h);
 uint32_t lk_lm_head_rows(uint32_t type, uint32_t h);
 uint32_t lk_lm_head_blocks(uint32_t vocab, uint32_t type, uint32_t h);
 hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t st);
+// The final norm and lm_head of 1..LK_HEAD_ROWS_MAX rows (rows of a.x h floats
+// apart) into logits rows a.vocab floats apart; no argmax, nothing deferred
+// (a.keys, a.epoch, a.st unused).
+#define LK_HEAD_ROWS_MAX 2u
+bool lk_lm_head_rows_fits(uint32_t type, uint32_t h, uint32_t nrows);
+hipError_t lk_lm_head_rows_launch(const LkHeadArgs& a, uint32_t nrows, uint32_t blocks, hipStream_t st);
 // Folds the keys of a deferred lm_head launch of `blocks` blocks into the
 // state (if it is pending) and advances the key epoch: the end of a run of
 // one-kernel steps.  One small launch.

@@ -251,6 +251,118 @@ __global__ __launch_bounds__(1024) void head_finish_kernel(const LkHeadArgs a, u
     *a.epoch = ep;
 }
 
+// The final norm and lm_head of NB activation rows at once (the Batcher's
+// 2-row steps): rows x + b*h of a.x (b < nrows) normalised into LDS by every
+// block, each weight row read once and dotted with all NB rows, logits row b at
+// a.logits + b*vocab (the GEMM's layout, read by the greedy launch that
+// follows).  Rows b >= nrows are computed from row nrows-1 and not stored.
+// Same norm arithmetic as lm_head_kernel; no argmax here.
+template <int WT, int NCH, int R, int NB>
+__global__ __launch_bounds__(HT) void lm_head_rows_kernel(const LkHeadArgs a, uint32_t nrows) {
+    extern __shared__ __align__(16) float xn[];  // NB * h floats
+    __shared__ float red[NB][HW];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t h = a.h, V = a.vocab;
+    const uint32_t gw = blockIdx.x * HW + (uint32_t)wave, nw = gridDim.x * HW;
+
+    constexpr int XPT = (int)(LK_HEAD_MAX_H / HT);
+    float xv[NB][XPT], gv[XPT];
+#pragma unroll
+    for (int k = 0; k < XPT; k++) {
+        const uint32_t i = threadIdx.x + (uint32_t)k * HT;
+        gv[k] = i < h ? a.norm[i] : 0.f;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const uint32_t rb = (uint32_t)b < nrows ? (uint32_t)b : nrows - 1;
+            xv[b][k] = i < h ? a.x[(size_t)rb * h + i] : 0.f;
+        }
+    }
+    Row<WT, NCH> rr[R];
+    uint32_t r0 = gw * R;
+#pragma unroll
+    for (int k = 0; k < R; k++) row_issue(rr[k], a.w, r0 + k < V ? r0 + k : V - 1, lane);
+
+    // math::rmsnorm (src/math.rs:45-49) per row, as in lm_head_kernel
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < XPT; k++) ss = fmaf(xv[b][k], xv[b][k], ss);
+        ss = lk_wave_sum(ss);
+        if (lane == 0) red[b][wave] = ss;
+    }
+    lds_only_barrier();
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < HW; i++) tot += red[b][i];
+        const float scale = 1.0f / sqrtf(tot / (float)h + a.eps);
+#pragma unroll
+        for (int k = 0; k < XPT; k++) {
+            const uint32_t i = threadIdx.x + (uint32_t)k * HT;
+            if (i < h) xn[(size_t)b * h + i] = __fmul_rn(__fmul_rn(xv[b][k], scale), gv[k]);
+        }
+    }
+    lds_only_barrier();
+
+    constexpr uint32_t CE = ChunkTraits<WT>::elems;
+    float xr[NB][NCH][CE];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const float* xb = xn + (size_t)b * h;
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const uint32_t ch = (uint32_t)lane + 64u * i;
+            const bool ok = ch < h / CE;
+            if constexpr (WT == LK_Q4_K) {
+                const uint32_t sb = ch >> 3, k = ch & 7;
+                const float* xl = xb + (ok ? sb * 256 + (k >> 1) * 64 + (k & 1) * 16 : 0);
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    xr[b][i][e] = ok ? xl[e] : 0.f;
+                    xr[b][i][16 + e] = ok ? xl[32 + e] : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < (int)CE; e++) xr[b][i][e] = ok ? xb[ch * CE + e] : 0.f;
+            }
+        }
+    }
+
+    const uint32_t step = nw * R;
+    for (; r0 < V; r0 += step) {
+        if (r0 != gw * R) {
+#pragma unroll
+            for (int k = 0; k < R; k++) row_issue(rr[k], a.w, r0 + k < V ? r0 + k : V - 1, lane);
+        }
+        float d[R][NB];
+#pragma unroll
+        for (int k = 0; k < R; k++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) d[k][b] = row_dot_reg(rr[k], xr[b], h, lane);
+        // wave sums (each equals lk_wave_sum's), then lane b*R + k stores (k, b)
+        float out = 0.f;
+#pragma unroll
+        for (int k = 0; k < R; k++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                float v = d[k][b];
+                v += lk_dpp<0xB1, 0xF>(v, 0.f);
+                v += lk_dpp<0x4E, 0xF>(v, 0.f);
+                v += lk_dpp<0x124, 0xF>(v, 0.f);
+                v += lk_dpp<0x128, 0xF>(v, 0.f);
+                v += lk_dpp<0x142, 0xA>(v, 0.f);
+                v += lk_dpp<0x143, 0xC>(v, 0.f);
+                v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+                out = lane == b * R + k ? v : out;
+            }
+        const uint32_t ob = (uint32_t)lane / R, ok_ = (uint32_t)lane % R;
+        if ((uint32_t)lane < (uint32_t)(R * NB) && ob < nrows && r0 + ok_ < V) a.logits[(size_t)ob * V + r0 + ok_] = out;
+    }
+}
+
 template <int WT, int NCH, int R>
 hipError_t launch(const LkHeadArgs& a, unsigned blocks, hipStream_t st) {
     hipLaunchKernelGGL((lm_head_kernel<WT, NCH, R>), dim3(blocks), dim3(HT), a.h * sizeof(float), st, a);
@@ -300,6 +412,41 @@ hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t s
     if (t == LK_Q4_K) { LKH_NCH(LK_Q4_K) }
     if (t == LK_Q8_SM) { LKH_NCH(LK_Q8_SM) }
 #undef LKH_NCH
+    return hipErrorInvalidValue;
+}
+
+// Two activation rows at most: a third and fourth make the kernel VALU-bound
+// (each 16-weight chunk then costs 64 FMAs and four wave reductions per lane;
+// Qwen2.5-0.5B shape, 3 / 4 rows: 0.744 / 0.754 ms per step against 0.728 /
+// 0.738 with the norm launch + MFMA GEMM, measured), and NCH <= 2 keeps both
+// rows' x slices in registers (Q4_K's NCH = 2 instance spilled).
+bool lk_lm_head_rows_fits(uint32_t type, uint32_t h, uint32_t nrows) {
+    if (!lk_lm_head_fits(type, h) || nrows == 0 || nrows > LK_HEAD_ROWS_MAX) return false;
+    const uint32_t nch = (h / head_chunk_elems(type) + 63) / 64;
+    return nch == 1 || (nch == 2 && type != LK_Q4_K);
+}
+
+namespace lkh {
+template <int T>
+hipError_t launch_rows(const LkHeadArgs& a, uint32_t nrows, uint32_t nch, uint32_t blocks, hipStream_t st) {
+    const size_t lds = 2 * (size_t)a.h * sizeof(float);
+    if (nch == 1)
+        hipLaunchKernelGGL((lm_head_rows_kernel<T, 1, 4, 2>), dim3(blocks), dim3(HT), lds, st, a, nrows);
+    else if constexpr (T != LK_Q4_K)
+        hipLaunchKernelGGL((lm_head_rows_kernel<T, 2, 2, 2>), dim3(blocks), dim3(HT), lds, st, a, nrows);
+    return hipGetLastError();
+}
+}  // namespace lkh
+
+hipError_t lk_lm_head_rows_launch(const LkHeadArgs& a, uint32_t nrows, uint32_t blocks, hipStream_t st) {
+    if (!lk_lm_head_rows_fits(a.w.type, a.h, nrows) || blocks == 0 || blocks > LK_HEAD_MAX_BLOCKS)
+        return hipErrorInvalidValue;
+    const uint32_t t = a.w.type;
+    const uint32_t nch = (a.h / head_chunk_elems(t) + 63) / 64;
+    if (t == LK_Q8_0) return lkh::launch_rows<LK_Q8_0>(a, nrows, nch, blocks, st);
+    if (t == LK_F16) return lkh::launch_rows<LK_F16>(a, nrows, nch, blocks, st);
+    if (t == LK_Q4_K) return lkh::launch_rows<LK_Q4_K>(a, nrows, nch, blocks, st);
+    if (t == LK_Q8_SM) return lkh::launch_rows<LK_Q8_SM>(a, nrows, nch, blocks, st);
     return hipErrorInvalidValue;
 }
 

@@ -177,6 +177,39 @@ def build(kind, seed=0):
 
 
 @pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n_rows", [2, 3])
+def test_batcher_head_rows_kernel_matches_the_gemm_head(kind, n_rows, monkeypatch):
+    """The 2-row one-kernel step ends with lm_head_rows_kernel (final norm +
+    lm_head of both rows in one launch; 3 rows keep the GEMM either way);
+    LKHIP_HEAD_ROWS=0 keeps the norm launch + lm_head GEMM.  Same rows, same steps: logits within 1e-5 of each
+    other (different summation orders), the oracle within the f16-KV bound."""
+    set_batch_path(monkeypatch, "fused")
+    cfg, eng, om = build(kind, seed=40 + n_rows)
+    rng = np.random.default_rng(40 + n_rows)
+    lens = [33, 70, 5, 64][:n_rows]
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.uint32) for n in lens]
+    toks = [[int(rng.integers(0, cfg.vocab_size)) for _ in lens] for _ in range(3)]
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LKHIP_HEAD_ROWS", mode)
+        bat = eng.batcher(4, 128)
+        for i, p in enumerate(prompts):
+            bat.prefill(i, p)
+        outs[mode] = [bat.decode_step([BatchRow(t[i], lens[i] + k, i) for i in range(n_rows)])
+                      for k, t in enumerate(toks)]
+        bat.close()
+    orc = [om.session(128, kv_f16=True) for _ in lens]
+    for i, p in enumerate(prompts):
+        orc[i].prefill(p)
+    for k, t in enumerate(toks):
+        for i in range(n_rows):
+            assert rel_err(outs["1"][k][i], outs["0"][k][i]) < 1e-5, (k, i)
+            assert rel_err(outs["1"][k][i], orc[i].forward(t[i], lens[i] + k)) < TOL_F16_KV, (k, i)
+    eng.close()
+    om.close()
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
 @pytest.mark.parametrize("n", [1, 37, 600])
 def test_chunked_prefill_matches_oracle(kind, n):
     """Prefill through the rows path (512-position chunks) against the CPU
