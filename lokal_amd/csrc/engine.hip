@@ -1552,7 +1552,8 @@ struct lkhip_batch {
     std::vector<hipGraphExec_t> step_graph;    // by row count: logits of every row
     std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
     // the multi-row one-kernel step (fused_rows.hip) for up to LK_FUSED_ROWS rows
-    bool fused_ok = false;
+    bool fused_ok = false;            // any of the three kernels below runs here
+    bool fused_k_ok[3] = {false, false, false};
     size_t fused_lds[3] = {0, 0, 0};  // 2-row, 4-row and LK_FUSED_ROWS-row kernels
     uint32_t fused_chunks = 0;
     DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
@@ -1813,7 +1814,7 @@ static hipError_t batch_enqueue_bstep(lkhip_batch* b, uint32_t n, hipStream_t st
 // each row over the call): one wave per (row, head, 64-position tile).
 static bool batch_fused_fits(const lkhip_batch* b, const std::vector<size_t>& last_pos) {
     if (last_pos.size() == 1 && b->single_ok) return true;  // the single-row step (any position)
-    if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS) return false;
+    if (!b->fused_ok || last_pos.size() > LK_FUSED_ROWS || !b->fused_k_ok[rows_kernel(last_pos.size())]) return false;
     const lkhip_config& c = b->e->cfg;
     const size_t nb = kRowsNb[rows_kernel(last_pos.size())];
     size_t items = (nb - last_pos.size()) * c.num_attention_heads;  // padding rows
@@ -1964,13 +1965,18 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         const size_t h = c.hidden_size, I = c.intermediate_size, nb = LK_FUSED_ROWS;
         const size_t qkvd = e->qd + 2 * e->kvd;
         b->fused_chunks = (uint32_t)(kv_seq / 64);
+        // each row count's kernel on its own: the 8-row one's LDS can exceed
+        // a CU's where the 2- and 4-row ones fit (TinyLlama's widths)
         LkFusedArgs probe{};
-        bool ok = true;
-        for (int k = 0; k < 3 && ok; k++) {
+        bool ok = false;
+        for (int k = 0; k < 3; k++) {
             const uint32_t kb = kRowsNb[k];
             b->fused_lds[k] = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, kb);
-            ok = lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi, e->fused_g, kb,
-                                      e->fused_blocks, b->fused_lds[k], nullptr, true) == hipSuccess;
+            b->fused_k_ok[k] = lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi,
+                                                    e->fused_g, kb, e->fused_blocks, b->fused_lds[k], nullptr,
+                                                    true) == hipSuccess;
+            if (!b->fused_k_ok[k]) (void)hipGetLastError();
+            ok |= b->fused_k_ok[k];
         }
         if (ok) {
             if ((rc = dev_alloc(b->fxb, 2 * nb * h * 8)) || (rc = dev_alloc(b->fqb, 2 * nb * qkvd * 8)) ||

@@ -531,7 +531,8 @@ static hipError_t launch_rows_t(const LkFusedArgs& a, unsigned blocks, size_t ld
 // hidden / intermediate width, GQA group), f16 KV, 2, 4 or LK_FUSED_ROWS rows.
 #define LKR_SHAPES(X)                       \
     X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */ \
-    X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */
+    X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */ \
+    X(LK_Q4_K, 1, 3, 8)  /* TinyLlama-1.1B */
 
 hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int nchi, int G, uint32_t nb,
                                 unsigned blocks, size_t lds, hipStream_t st, bool setup) {
