@@ -419,11 +419,12 @@ hipError_t lk_lm_head_launch(const LkHeadArgs& a, uint32_t blocks, hipStream_t s
 // (each 16-weight chunk then costs 64 FMAs and four wave reductions per lane;
 // Qwen2.5-0.5B shape, 3 / 4 rows: 0.744 / 0.754 ms per step against 0.728 /
 // 0.738 with the norm launch + MFMA GEMM, measured), and NCH <= 2 keeps both
-// rows' x slices in registers (Q4_K's NCH = 2 instance spilled).
+// rows' x slices in registers.  Not Q4_K: its dequant makes even two rows
+// VALU-bound (TinyLlama shape, 2 rows: 0.899 against 0.890 ms per step).
 bool lk_lm_head_rows_fits(uint32_t type, uint32_t h, uint32_t nrows) {
-    if (!lk_lm_head_fits(type, h) || nrows == 0 || nrows > LK_HEAD_ROWS_MAX) return false;
+    if (type == LK_Q4_K || !lk_lm_head_fits(type, h) || nrows == 0 || nrows > LK_HEAD_ROWS_MAX) return false;
     const uint32_t nch = (h / head_chunk_elems(type) + 63) / 64;
-    return nch == 1 || (nch == 2 && type != LK_Q4_K);
+    return nch <= 2;
 }
 
 namespace lkh {
@@ -432,7 +433,7 @@ hipError_t launch_rows(const LkHeadArgs& a, uint32_t nrows, uint32_t nch, uint32
     const size_t lds = 2 * (size_t)a.h * sizeof(float);
     if (nch == 1)
         hipLaunchKernelGGL((lm_head_rows_kernel<T, 1, 4, 2>), dim3(blocks), dim3(HT), lds, st, a, nrows);
-    else if constexpr (T != LK_Q4_K)
+    else
         hipLaunchKernelGGL((lm_head_rows_kernel<T, 2, 2, 2>), dim3(blocks), dim3(HT), lds, st, a, nrows);
     return hipGetLastError();
 }
@@ -445,7 +446,6 @@ hipError_t lk_lm_head_rows_launch(const LkHeadArgs& a, uint32_t nrows, uint32_t 
     const uint32_t nch = (a.h / head_chunk_elems(t) + 63) / 64;
     if (t == LK_Q8_0) return lkh::launch_rows<LK_Q8_0>(a, nrows, nch, blocks, st);
     if (t == LK_F16) return lkh::launch_rows<LK_F16>(a, nrows, nch, blocks, st);
-    if (t == LK_Q4_K) return lkh::launch_rows<LK_Q4_K>(a, nrows, nch, blocks, st);
     if (t == LK_Q8_SM) return lkh::launch_rows<LK_Q8_SM>(a, nrows, nch, blocks, st);
     return hipErrorInvalidValue;
 }
