@@ -31,8 +31,15 @@
 #define LKR_KB_F16 2
 #define LKR_KA_F16 2
 #endif
-#define LKR_KB (WT == LK_F16 ? LKR_KB_F16 : 3)
-#define LKR_KA (WT == LK_F16 ? LKR_KA_F16 : 2)
+// Q4_K: one of each (its rows are wider; holding 3 + 2 spilled 68 bytes per
+// lane, 2 + 2 24 bytes; TinyLlama shape, 2 / 4 rows: 0.894 / 1.337 ms per step
+// at 3 + 2, 0.857 / 1.318 at 2 + 2, 0.852 / 1.312 at 1 + 1, measured)
+#ifndef LKR_KB_Q4K
+#define LKR_KB_Q4K 1
+#define LKR_KA_Q4K 1
+#endif
+#define LKR_KB (WT == LK_F16 ? LKR_KB_F16 : (WT == LK_Q4_K ? LKR_KB_Q4K : 3))
+#define LKR_KA (WT == LK_F16 ? LKR_KA_F16 : (WT == LK_Q4_K ? LKR_KA_Q4K : 2))
 
 namespace lkf {
 
