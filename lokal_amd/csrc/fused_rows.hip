@@ -535,7 +535,7 @@ static hipError_t launch_rows_t(const LkFusedArgs& a, unsigned blocks, size_t ld
 }
 
 // Instantiated shapes: (weight type, 16-byte chunks per lane for rows of
-// hidden / intermediate width, GQA group), f16 KV, 2, 4 or LK_FUSED_ROWS rows.
+// hidden / intermediate width, GQA group), f16 KV, 2, 3, 4 or LK_FUSED_ROWS rows.
 #define LKR_SHAPES(X)                       \
     X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */ \
     X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */ \
@@ -545,7 +545,8 @@ hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int
                                 unsigned blocks, size_t lds, hipStream_t st, bool setup) {
 #define X(T, NH, NI, GG)                                                                           \
     if (wt == T && nchh == NH && nchi == NI && G == GG)                                            \
-        return nb <= 2   ? launch_rows_t<T, NH, NI, GG, 2>(a, blocks, lds, st, setup)              \
+        return nb <= 2    ? launch_rows_t<T, NH, NI, GG, 2>(a, blocks, lds, st, setup)             \
+               : nb == 3 ? launch_rows_t<T, NH, NI, GG, 3>(a, blocks, lds, st, setup)              \
                : nb <= 4 ? launch_rows_t<T, NH, NI, GG, 4>(a, blocks, lds, st, setup)              \
                          : launch_rows_t<T, NH, NI, GG, LK_FUSED_ROWS>(a, blocks, lds, st, setup);
     LKR_SHAPES(X)
