@@ -41,6 +41,13 @@
 #define LKR_KB (WT == LK_F16 ? LKR_KB_F16 : (WT == LK_Q4_K ? LKR_KB_Q4K : 3))
 #define LKR_KA (WT == LK_F16 ? LKR_KA_F16 : (WT == LK_Q4_K ? LKR_KA_Q4K : 2))
 
+// Rows of the SwiGLU input the down stage takes per pass: a divisor of NB
+// (every pass is whole rows that exist), at most 4 where NB allows it, so the
+// 8-row kernel's LDS fits (2 passes of 4; 6 rows: 2 of 3; 5 rows: 1 of 5).
+__host__ __device__ constexpr int lkr_s6_rows(int nb) {
+    return nb <= 4 ? nb : (nb % 4 == 0 ? 4 : (nb % 3 == 0 ? 3 : (nb % 2 == 0 ? 2 : nb)));
+}
+
 namespace lkf {
 
 using namespace lk;
@@ -51,7 +58,8 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
     const uint32_t h = a.h, I = a.I, nh = a.nh, nkv = a.nkv;
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
     // the down stage takes its input S6R rows at a time, so that NB = 8 fits
-    constexpr int S6R = NB < 4 ? NB : 4;
+    constexpr int S6R = lkr_s6_rows(NB);
+    static_assert(NB % S6R == 0, "the down stage's passes cover whole rows that exist");
     const uint32_t hq_max = h > qd ? h : qd;
     const uint32_t xin_n = NB * hq_max > S6R * I ? NB * hq_max : S6R * I;
     float* xin = lds;                   // xin_n: the (normalised) input rows of a stage
@@ -512,7 +520,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
 }  // namespace lkf
 
 size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb) {
-    const size_t s6r = nb < 4 ? nb : 4;
+    const size_t s6r = (size_t)lkr_s6_rows((int)nb);
     const size_t hq_max = h > nh * 64 ? h : nh * 64;
     const size_t xin_n = std::max((size_t)nb * hq_max, s6r * I);
     return (xin_n + (size_t)nb * h + (size_t)nb * FW + 2 * (size_t)h + (size_t)FW * 256) * 4 +
@@ -548,6 +556,8 @@ hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int
         return nb <= 2    ? launch_rows_t<T, NH, NI, GG, 2>(a, blocks, lds, st, setup)             \
                : nb == 3 ? launch_rows_t<T, NH, NI, GG, 3>(a, blocks, lds, st, setup)              \
                : nb <= 4 ? launch_rows_t<T, NH, NI, GG, 4>(a, blocks, lds, st, setup)              \
+               : nb == 5 ? launch_rows_t<T, NH, NI, GG, 5>(a, blocks, lds, st, setup)              \
+               : nb == 6 ? launch_rows_t<T, NH, NI, GG, 6>(a, blocks, lds, st, setup)              \
                          : launch_rows_t<T, NH, NI, GG, LK_FUSED_ROWS>(a, blocks, lds, st, setup);
     LKR_SHAPES(X)
 #undef X
