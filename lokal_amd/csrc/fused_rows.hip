@@ -543,7 +543,7 @@ static hipError_t launch_rows_t(const LkFusedArgs& a, unsigned blocks, size_t ld
 }
 
 // Instantiated shapes: (weight type, 16-byte chunks per lane for rows of
-// hidden / intermediate width, GQA group), f16 KV, 2, 3, 4 or LK_FUSED_ROWS rows.
+// hidden / intermediate width, GQA group), f16 KV, 2, 3, 4, 5, 6 or LK_FUSED_ROWS rows.
 #define LKR_SHAPES(X)                       \
     X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */ \
     X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */ \
