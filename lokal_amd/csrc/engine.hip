@@ -1553,8 +1553,8 @@ struct lkhip_batch {
     std::vector<hipGraphExec_t> greedy_graph;  // by row count: + argmax fed back
     // the multi-row one-kernel step (fused_rows.hip) for up to LK_FUSED_ROWS rows
     bool fused_ok = false;            // any of the three kernels below runs here
-    bool fused_k_ok[6] = {false, false, false, false, false, false};
-    size_t fused_lds[6] = {0, 0, 0, 0, 0, 0};  // 2-, 3-, 4-, 5-, 6- and LK_FUSED_ROWS-row kernels
+    bool fused_k_ok[7] = {false, false, false, false, false, false, false};
+    size_t fused_lds[7] = {0, 0, 0, 0, 0, 0, 0};  // 2- to 7- and LK_FUSED_ROWS-row kernels
     uint32_t fused_chunks = 0;
     DevBuf fxb, fqb, fpb, fab, fxpb, fib, fepoch, ferr;
     // a step of one row: the single-row one-kernel step (fused.hip) on the
@@ -1613,8 +1613,8 @@ static bool graphs_on() {
 // leaving the final x rows in rows.x.
 // Rows of the multi-row one-kernel step's instances, and the one that serves
 // n rows (fewer are padded).
-static constexpr uint32_t kRowsNb[6] = {2, 3, 4, 5, 6, LK_FUSED_ROWS};
-static int rows_kernel(size_t n) { return n <= 2 ? 0 : n <= 6 ? (int)n - 2 : 5; }
+static constexpr uint32_t kRowsNb[7] = {2, 3, 4, 5, 6, 7, LK_FUSED_ROWS};
+static int rows_kernel(size_t n) { return n <= 2 ? 0 : n <= 7 ? (int)n - 2 : 6; }
 
 static hipError_t batch_enqueue_fused(lkhip_batch* b, uint32_t n, hipStream_t st) {
     const lkhip_engine* e = b->e;
@@ -1969,7 +1969,7 @@ extern "C" int lkhip_batch_create(lkhip_engine* e, size_t n_slots, size_t max_se
         // a CU's where the 2- and 4-row ones fit (TinyLlama's widths)
         LkFusedArgs probe{};
         bool ok = false;
-        for (int k = 0; k < 6; k++) {
+        for (int k = 0; k < 7; k++) {
             const uint32_t kb = kRowsNb[k];
             b->fused_lds[k] = lk_fused_rows_lds_bytes(c.hidden_size, c.intermediate_size, c.num_attention_heads, kb);
             b->fused_k_ok[k] = lk_fused_rows_launch(probe, e->layers[0].q->dw.type, e->fused_nchh, e->fused_nchi,

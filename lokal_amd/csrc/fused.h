@@ -102,7 +102,7 @@ __host__ __device__ constexpr uint32_t lk_fused_unit(bool kv_f32) { return kv_f3
 int lk_fused_threads();
 // Writes the XCD id (0..15) of each workgroup of a `blocks`-workgroup launch.
 hipError_t lk_xcd_probe_launch(uint32_t* out, unsigned blocks, hipStream_t st);
-// The multi-row one-kernel step (fused_rows.hip): 2, 3, 4, 5, 6 or LK_FUSED_ROWS
+// The multi-row one-kernel step (fused_rows.hip): 2-7 or LK_FUSED_ROWS
 // Batcher rows per launch (fewer are padded), f16 KV.
 #define LK_FUSED_ROWS 8u
 size_t lk_fused_rows_lds_bytes(uint32_t h, uint32_t I, uint32_t nh, uint32_t nb);

@@ -41,11 +41,12 @@
 #define LKR_KB (WT == LK_F16 ? LKR_KB_F16 : (WT == LK_Q4_K ? LKR_KB_Q4K : 3))
 #define LKR_KA (WT == LK_F16 ? LKR_KA_F16 : (WT == LK_Q4_K ? LKR_KA_Q4K : 2))
 
-// Rows of the SwiGLU input the down stage takes per pass: a divisor of NB
-// (every pass is whole rows that exist), at most 4 where NB allows it, so the
-// 8-row kernel's LDS fits (2 passes of 4; 6 rows: 2 of 3; 5 rows: 1 of 5).
+// Rows of the SwiGLU input the down stage takes per pass (the last pass takes
+// what is left, so every pass covers rows that exist): at most 4 where the
+// LDS needs it (8 rows: 2 passes of 4; 7 rows: 4 + 3; 6 rows: 3 + 3; 5 rows:
+// one pass of 5).
 __host__ __device__ constexpr int lkr_s6_rows(int nb) {
-    return nb <= 4 ? nb : (nb % 4 == 0 ? 4 : (nb % 3 == 0 ? 3 : (nb % 2 == 0 ? 2 : nb)));
+    return nb <= 5 ? nb : (nb == 6 ? 3 : 4);
 }
 
 namespace lkf {
@@ -59,7 +60,6 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
     const uint32_t qd = nh * 64, kvd = nkv * 64, qkvd = qd + 2 * kvd;
     // the down stage takes its input S6R rows at a time, so that NB = 8 fits
     constexpr int S6R = lkr_s6_rows(NB);
-    static_assert(NB % S6R == 0, "the down stage's passes cover whole rows that exist");
     const uint32_t hq_max = h > qd ? h : qd;
     const uint32_t xin_n = NB * hq_max > S6R * I ? NB * hq_max : S6R * I;
     float* xin = lds;                   // xin_n: the (normalised) input rows of a stage
@@ -485,10 +485,11 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
             };
 #pragma unroll 1
             for (int p0 = 0; p0 < NB; p0 += S6R) {  // S6R rows of the SwiGLU input at a time
-                stage_in<24>(c, IB + (size_t)p0 * I, S6R * I, ep, xin, -1);
+                const int nr = NB - p0 < S6R ? NB - p0 : S6R;  // the last pass: the rows left
+                stage_in<24>(c, IB + (size_t)p0 * I, (uint32_t)nr * I, ep, xin, -1);
                 if (c.gw < (int)h) {
 #pragma unroll 1
-                    for (int b = 0; b < S6R; b++) {
+                    for (int b = 0; b < nr; b++) {
                         const float d = lk_wave_sum(row_dot(dn, xin + b * I, I, lane));
                         if (lane == 0) put(p0 + b, c.gw, xres[(p0 + b) * h + c.gw] + d);
                     }
@@ -497,7 +498,7 @@ __global__ __launch_bounds__(FT, 1) void fused_rows_kernel(const LkFusedArgs a) 
                     Row<WT, NCHI> rr;
                     row_issue(rr, ly.down, (uint32_t)uu, lane);
 #pragma unroll 1
-                    for (int b = 0; b < S6R; b++) {
+                    for (int b = 0; b < nr; b++) {
                         const float d = lk_wave_sum(row_dot(rr, xin + b * I, I, lane));
                         if (lane == 0) put(p0 + b, uu, xres[(p0 + b) * h + uu] + d);
                     }
@@ -543,7 +544,7 @@ static hipError_t launch_rows_t(const LkFusedArgs& a, unsigned blocks, size_t ld
 }
 
 // Instantiated shapes: (weight type, 16-byte chunks per lane for rows of
-// hidden / intermediate width, GQA group), f16 KV, 2, 3, 4, 5, 6 or LK_FUSED_ROWS rows.
+// hidden / intermediate width, GQA group), f16 KV, 2-7 or LK_FUSED_ROWS rows.
 #define LKR_SHAPES(X)                       \
     X(LK_Q8_0, 1, 5, 7)  /* Qwen2.5-0.5B */ \
     X(LK_F16, 2, 3, 3)   /* SmolLM2-135M */ \
@@ -558,6 +559,7 @@ hipError_t lk_fused_rows_launch(const LkFusedArgs& a, uint32_t wt, int nchh, int
                : nb <= 4 ? launch_rows_t<T, NH, NI, GG, 4>(a, blocks, lds, st, setup)              \
                : nb == 5 ? launch_rows_t<T, NH, NI, GG, 5>(a, blocks, lds, st, setup)              \
                : nb == 6 ? launch_rows_t<T, NH, NI, GG, 6>(a, blocks, lds, st, setup)              \
+               : nb == 7 ? launch_rows_t<T, NH, NI, GG, 7>(a, blocks, lds, st, setup)              \
                          : launch_rows_t<T, NH, NI, GG, LK_FUSED_ROWS>(a, blocks, lds, st, setup);
     LKR_SHAPES(X)
 #undef X

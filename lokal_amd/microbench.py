@@ -358,7 +358,7 @@ def batch() -> list[dict]:
     out = []
     steps = 64
     import os
-    rows_list = [int(v) for v in os.environ.get("LKHIP_MB_ROWS", "1,2,3,4,5,6,8,16,32,64").split(",")]
+    rows_list = [int(v) for v in os.environ.get("LKHIP_MB_ROWS", "1,2,3,4,5,6,7,8,16,32,64").split(",")]
     for B in rows_list:
         bat = eng.batcher(B, 512 + steps + 16)
         first = []
